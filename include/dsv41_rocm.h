@@ -1,0 +1,141 @@
+/*
+ * dsv41_rocm.h — C ABI of libdsv41hip.so, the MI355X (gfx950) implementation of
+ * Tiny-DSV41's token-sampling step and fused selected-token log-prob head.
+ *
+ * Plain C: pointers, sizes and PODs only. Every device pointer is a HIP device
+ * address owned by the caller; the library never allocates or frees device
+ * memory, never synchronises the stream, and launches only on `stream`.
+ *
+ * Return codes: 0 on success, a negative DSV41_E_* code before any launch on a
+ * bad argument. dsv41_last_error() then holds a thread-local message whose text
+ * mirrors the reference's ValueError messages where one exists.
+ *
+ * Reference interfaces replaced (paths relative to the Tiny-DSV41 tree):
+ *   dsv41_sampler_run  <- dsv41_train/rl/rollout.py:144-150 (log_softmax(logits/T),
+ *                         isfinite check, multinomial draw, behaviour log-prob),
+ *                         extended with the vLLM SamplingParams knobs named at
+ *                         rollout_manager/backends/vllm_actor.py:178-185.
+ *   dsv41_logprob_run  <- dsv41_train/models/dsv4/model.py:679-684 (_token_log_probs),
+ *                         dsv41_train/rl/native_lora.py:80-82 (_score_targets),
+ *                         plus the Token-TIS weight of dsv41_train/rl/algorithm.py:293-299.
+ */
+#ifndef DSV41_ROCM_H
+#define DSV41_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSV41_ABI_VERSION 1
+
+/* Element types of logits / activations. */
+#define DSV41_DTYPE_F32 0
+#define DSV41_DTYPE_BF16 1
+
+/* Error codes (negative returns). */
+#define DSV41_OK 0
+#define DSV41_E_INVALID (-1)     /* bad shape, stride, pointer or parameter value   */
+#define DSV41_E_UNSUPPORTED (-2) /* valid request beyond on-chip limits of a kernel  */
+#define DSV41_E_WORKSPACE (-3)   /* workspace missing or smaller than required       */
+#define DSV41_E_HIP (-4)         /* a HIP runtime call failed                        */
+#define DSV41_E_ABI (-5)         /* descriptor struct_size does not match this build  */
+
+/* Per-row / per-token status bits written to out_status (0 = clean). */
+#define DSV41_STATUS_NONFINITE 1   /* a processed logit / result was NaN or +-inf      */
+#define DSV41_STATUS_BAD_HISTORY 2 /* a history id was >= vocab (id ignored)           */
+#define DSV41_STATUS_BAD_UNIFORM 4 /* uniform outside [0, 1) (row drawn with u = 0)    */
+#define DSV41_STATUS_RATIO_ZERO 8  /* Token-TIS raw weight exp(old - behaviour) == 0   */
+
+/*
+ * Row sampler.  For each row r of logits[rows, vocab]:
+ *   x = float(logit); for ids with count c > 0 in the row's history:
+ *     x = x > 0 ? x / repetition_penalty : x * repetition_penalty;
+ *     x = x - frequency_penalty * c;  x = x - presence_penalty;
+ *   z = x / temperature;
+ *   min-p  (min_p > 0): keep z_i - z_max >= log(min_p) (fp64);
+ *   top-k  (top_k > 0): keep the first top_k of the survivors in (z desc, index asc);
+ *   top-p  (top_p < 1): keep the shortest prefix of that order whose 2^-43 fixed-point
+ *                       mass reaches ceil(top_p * total);
+ *   draw: inverse CDF in vocabulary order over the kept set against uniforms[r]
+ *         (greedy != 0: first index of max z instead);
+ *   out_logprob = z_tok - log(sum_kept exp(z)), out_kept = kept-set size.
+ * history[r * history_row_stride + j], j < (history_lens ? history_lens[r] : hist_len);
+ * negative ids are padding and ignored.
+ */
+typedef struct dsv41_sampler_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_sampler_desc) */
+  int32_t rows;
+  int32_t vocab;
+  int32_t logits_dtype;        /* DSV41_DTYPE_F32 or DSV41_DTYPE_BF16 */
+  int64_t logits_row_stride;   /* in elements */
+  const void* logits;          /* [rows, vocab] */
+  const int64_t* history;      /* [rows, history_row_stride] or NULL */
+  int64_t history_row_stride;  /* in elements */
+  int32_t hist_len;            /* ids per row when history_lens == NULL */
+  const int32_t* history_lens; /* [rows] or NULL */
+  const float* uniforms;       /* [rows]; may be NULL only when greedy != 0 */
+  float temperature;           /* finite, > 0 */
+  float repetition_penalty;    /* finite, > 0; 1 = off */
+  float presence_penalty;      /* finite; 0 = off */
+  float frequency_penalty;     /* finite; 0 = off */
+  int32_t top_k;               /* 0 = off */
+  float top_p;                 /* (0, 1]; 1 = off */
+  float min_p;                 /* [0, 1]; 0 = off */
+  int32_t greedy;              /* nonzero: argmax instead of the draw */
+  int64_t* out_ids;            /* [rows] */
+  float* out_logprob;          /* [rows] */
+  int32_t* out_kept;           /* [rows] or NULL */
+  int32_t* out_status;         /* [rows] */
+} dsv41_sampler_desc;
+
+/*
+ * Fused selected-token log-prob.  logits = x[N,H] @ w[V,H]^T in fp32 (never stored),
+ * z = logits / temperature; for each token n:
+ *   out_logprob[n] = z[n, targets[n]] - logsumexp(z[n, :])
+ *   out_entropy[n] = logsumexp(z[n, :]) - sum_v softmax(z[n])_v * z[n, v]
+ *   out_ratio[n]   = float(min(is_cap, exp(double(float(out_logprob[n] - behavior[n])))))
+ *                    when behavior != NULL (Token-TIS weight, algorithm.py:293-299).
+ */
+typedef struct dsv41_logprob_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_logprob_desc) */
+  int32_t n_tokens;
+  int32_t hidden;
+  int32_t vocab;
+  const void* x;          /* bf16 [N, H] */
+  int64_t x_row_stride;   /* in elements, multiple of 8 */
+  const void* w;          /* bf16 [V, H] (nn.Linear weight layout) */
+  int64_t w_row_stride;   /* in elements, multiple of 8 */
+  const int64_t* targets; /* [N], each in [0, V) */
+  float temperature;      /* finite, > 0 */
+  const float* behavior;  /* [N] or NULL */
+  float is_cap;           /* finite, > 0 (used when behavior != NULL) */
+  float* out_logprob;     /* [N] */
+  float* out_entropy;     /* [N] or NULL */
+  float* out_ratio;       /* [N] or NULL; requires behavior */
+  int32_t* out_status;    /* [N] or NULL */
+} dsv41_logprob_desc;
+
+/* ABI identity. */
+int dsv41_abi_version(void);
+size_t dsv41_sampler_desc_size(void);
+size_t dsv41_logprob_desc_size(void);
+const char* dsv41_last_error(void);
+
+/* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch. */
+size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* desc);
+int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t workspace_bytes,
+                      void* stream /* hipStream_t */);
+
+/* Fused selected-token log-prob: replaces model.py:679-684 / native_lora.py:80-82. */
+size_t dsv41_logprob_workspace_bytes(const dsv41_logprob_desc* desc);
+int dsv41_logprob_run(const dsv41_logprob_desc* desc, void* workspace, size_t workspace_bytes,
+                      void* stream /* hipStream_t */);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV41_ROCM_H */

@@ -1,0 +1,12 @@
+"""dsv41_rocm — MI355X (gfx950) token sampler and fused selected-token log-prob.
+
+Drop-in for Tiny-DSV41's rollout sampling step (``dsv41_train/rl/rollout.py:144-150``) and
+its selected-token log-prob head (``dsv41_train/models/dsv4/model.py:679-684``,
+``dsv41_train/rl/native_lora.py:80-82``), backed by hand-written HIP kernels in
+``libdsv41hip.so`` (C ABI: ``include/dsv41_rocm.h``).
+"""
+
+from ._lib import load as load_library  # noqa: F401
+from .sampling import SampleResult, sample, sample_next, validate_temperature  # noqa: F401
+
+__all__ = ["SampleResult", "sample", "sample_next", "validate_temperature", "load_library"]

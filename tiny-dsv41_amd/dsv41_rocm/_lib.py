@@ -1,0 +1,155 @@
+"""ctypes binding of libdsv41hip.so (the C ABI declared in include/dsv41_rocm.h).
+
+The library is loaded from this package directory only.  There is no fallback:
+if the library is missing or was built for another ABI, every product entry point
+raises ``RuntimeError`` naming the file and the build step.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).with_name("libdsv41hip.so")
+ABI_VERSION = 1
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+OK = 0
+E_INVALID = -1
+E_UNSUPPORTED = -2
+E_WORKSPACE = -3
+E_HIP = -4
+E_ABI = -5
+
+STATUS_NONFINITE = 1
+STATUS_BAD_HISTORY = 2
+STATUS_BAD_UNIFORM = 4
+STATUS_RATIO_ZERO = 8
+
+
+class SamplerDesc(ctypes.Structure):
+    """Mirror of dsv41_sampler_desc."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("rows", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("logits_dtype", ctypes.c_int32),
+        ("logits_row_stride", ctypes.c_int64),
+        ("logits", ctypes.c_void_p),
+        ("history", ctypes.c_void_p),
+        ("history_row_stride", ctypes.c_int64),
+        ("hist_len", ctypes.c_int32),
+        ("history_lens", ctypes.c_void_p),
+        ("uniforms", ctypes.c_void_p),
+        ("temperature", ctypes.c_float),
+        ("repetition_penalty", ctypes.c_float),
+        ("presence_penalty", ctypes.c_float),
+        ("frequency_penalty", ctypes.c_float),
+        ("top_k", ctypes.c_int32),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("greedy", ctypes.c_int32),
+        ("out_ids", ctypes.c_void_p),
+        ("out_logprob", ctypes.c_void_p),
+        ("out_kept", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+    ]
+
+
+class LogprobDesc(ctypes.Structure):
+    """Mirror of dsv41_logprob_desc."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("n_tokens", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("x_row_stride", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("w_row_stride", ctypes.c_int64),
+        ("targets", ctypes.c_void_p),
+        ("temperature", ctypes.c_float),
+        ("behavior", ctypes.c_void_p),
+        ("is_cap", ctypes.c_float),
+        ("out_logprob", ctypes.c_void_p),
+        ("out_entropy", ctypes.c_void_p),
+        ("out_ratio", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+    ]
+
+
+EXPORTS = (
+    "dsv41_abi_version",
+    "dsv41_sampler_desc_size",
+    "dsv41_logprob_desc_size",
+    "dsv41_last_error",
+    "dsv41_sampler_workspace_bytes",
+    "dsv41_sampler_run",
+    "dsv41_logprob_workspace_bytes",
+    "dsv41_logprob_run",
+)
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
+    lib.dsv41_abi_version.restype = ctypes.c_int
+    lib.dsv41_sampler_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_logprob_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_last_error.restype = ctypes.c_char_p
+    lib.dsv41_sampler_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsv41_sampler_workspace_bytes.argtypes = [ctypes.POINTER(SamplerDesc)]
+    lib.dsv41_sampler_run.restype = ctypes.c_int
+    lib.dsv41_sampler_run.argtypes = [ctypes.POINTER(SamplerDesc), ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p]
+    lib.dsv41_logprob_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsv41_logprob_workspace_bytes.argtypes = [ctypes.POINTER(LogprobDesc)]
+    lib.dsv41_logprob_run.restype = ctypes.c_int
+    lib.dsv41_logprob_run.argtypes = [ctypes.POINTER(LogprobDesc), ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p]
+    return lib
+
+
+def load() -> ctypes.CDLL:
+    """Load and check libdsv41hip.so; raise RuntimeError when it is absent or stale."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.is_file():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `make -C {LIB_PATH.parent.parent}` "
+                "(or __graft_entry__.build()); there is no CPU fallback")
+        lib = _bind(ctypes.CDLL(os.fspath(LIB_PATH)))
+        if lib.dsv41_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {lib.dsv41_abi_version()}, expected {ABI_VERSION}")
+        if lib.dsv41_sampler_desc_size() != ctypes.sizeof(SamplerDesc):
+            raise RuntimeError("dsv41_sampler_desc layout differs between library and binding")
+        if lib.dsv41_logprob_desc_size() != ctypes.sizeof(LogprobDesc):
+            raise RuntimeError("dsv41_logprob_desc layout differs between library and binding")
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().dsv41_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int) -> None:
+    """Map a negative return code to the Python exception the reference raises."""
+    if rc == OK:
+        return
+    msg = last_error()
+    if rc in (E_INVALID, E_WORKSPACE):
+        raise ValueError(msg)
+    if rc == E_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(f"libdsv41hip error {rc}: {msg}")

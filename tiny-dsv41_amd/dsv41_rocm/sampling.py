@@ -1,0 +1,172 @@
+"""Token sampling on MI355X: the drop-in for the sampling step of ``generate_group``.
+
+Reference (paths relative to the Tiny-DSV41 tree):
+
+* ``dsv41_train/rl/rollout.py:144-150`` — ``log_probs = log_softmax(logits.float() / T)``,
+  non-finite check (:145-146, ``ValueError("generation log probabilities contain non-finite
+  values")``), ``multinomial`` draw with a CPU generator (:148), ``behavior = log_probs[token]``.
+* ``dsv41_train/rl/algorithm.py:19-21`` — ``validate_temperature``.
+* ``rollout_manager/backends/vllm_actor.py:178-185, :260`` — the SamplingParams knobs
+  (repetition / presence / frequency penalty, top-k, top-p, min-p) and processed log-probs.
+
+The draw is an inverse CDF in vocabulary order against one uniform per row.  Uniforms come
+from the caller or from a CPU ``torch.Generator`` (``torch.rand``), so a generator state
+persisted like the reference's (``rollout_manager/backends/pytorch_rl.py:70-72, :113-114``)
+replays the same tokens.  All arithmetic runs in libdsv41hip.so; this module validates
+arguments, allocates outputs with torch and launches on the current HIP stream.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+@dataclass
+class SampleResult:
+    """Per-row outputs: drawn ids (int64), their log-probs under the processed
+    distribution (fp32), kept-set sizes (int32) and status bits (int32)."""
+
+    ids: torch.Tensor
+    logprobs: torch.Tensor
+    kept: torch.Tensor
+    status: torch.Tensor
+
+
+def validate_temperature(temperature: float) -> None:
+    """Same rule and message as algorithm.py:19-21."""
+    if not math.isfinite(temperature) or temperature <= 0:
+        raise ValueError("temperature must be finite and positive")
+
+
+def _device_ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _status_error(status: torch.Tensor) -> None:
+    bits = 0
+    for v in status.cpu().tolist():
+        bits |= int(v)
+    if bits & _lib.STATUS_NONFINITE:
+        raise ValueError("generation log probabilities contain non-finite values")
+    if bits & _lib.STATUS_BAD_HISTORY:
+        raise ValueError("history token ID is outside the model vocabulary")
+    if bits & _lib.STATUS_BAD_UNIFORM:
+        raise ValueError("uniforms must lie in [0, 1)")
+
+
+def sample(
+    logits: torch.Tensor,
+    *,
+    temperature: float = 1.0,
+    uniforms: Optional[torch.Tensor] = None,
+    generator: Optional[torch.Generator] = None,
+    history: Optional[torch.Tensor] = None,
+    history_lens: Optional[torch.Tensor] = None,
+    repetition_penalty: float = 1.0,
+    presence_penalty: float = 0.0,
+    frequency_penalty: float = 0.0,
+    top_k: int = 0,
+    top_p: float = 1.0,
+    min_p: float = 0.0,
+    greedy: bool = False,
+    check: bool = True,
+) -> SampleResult:
+    """Sample one token per row of ``logits[rows, vocab]`` (fp32 or bf16, on the GPU).
+
+    ``history[rows, L]`` (int64, negative = padding) feeds the penalties; ``history_lens``
+    (int32 [rows]) optionally gives ragged lengths.  ``uniforms`` (fp32 [rows] in [0, 1))
+    drive the draw; when omitted they are drawn with ``torch.rand(rows, generator=generator)``
+    on the CPU.  With ``check`` the call synchronises and raises the reference's
+    ``ValueError`` for non-finite rows, out-of-vocabulary history or bad uniforms.
+    """
+    validate_temperature(temperature)
+    if not isinstance(logits, torch.Tensor) or logits.ndim != 2 or 0 in logits.shape:
+        raise ValueError("logits must have shape [rows, vocabulary_size]")
+    if not logits.is_cuda:
+        raise ValueError("logits must be on the GPU (libdsv41hip has no CPU path)")
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        logits = logits.float()
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    if isinstance(top_k, bool) or not isinstance(top_k, int) or top_k < 0:
+        raise ValueError("top_k must be a nonnegative integer")
+    rows, vocab = logits.shape
+    device = logits.device
+    if not greedy:
+        if uniforms is None:
+            if generator is not None and generator.device.type != "cpu":
+                raise ValueError("generation requires a CPU torch.Generator")
+            uniforms = torch.rand(rows, generator=generator, dtype=torch.float32)
+        uniforms = uniforms.to(device=device, dtype=torch.float32).contiguous()
+        if uniforms.shape != (rows,):
+            raise ValueError("one uniform is required per row")
+    if history is not None:
+        if history.ndim != 2 or history.shape[0] != rows:
+            raise ValueError("history must have shape [rows, history_length]")
+        history = history.to(device=device, dtype=torch.int64)
+        if history.stride(1) != 1:
+            history = history.contiguous()
+        if history_lens is not None:
+            history_lens = history_lens.to(device=device, dtype=torch.int32).contiguous()
+            if history_lens.shape != (rows,):
+                raise ValueError("history_lens must have one length per row")
+    ids = torch.empty(rows, dtype=torch.int64, device=device)
+    lps = torch.empty(rows, dtype=torch.float32, device=device)
+    kept = torch.empty(rows, dtype=torch.int32, device=device)
+    status = torch.empty(rows, dtype=torch.int32, device=device)
+    desc = _lib.SamplerDesc()
+    desc.struct_size = _lib.ctypes.sizeof(_lib.SamplerDesc)
+    desc.rows = rows
+    desc.vocab = vocab
+    desc.logits_dtype = _lib.DTYPE_F32 if logits.dtype == torch.float32 else _lib.DTYPE_BF16
+    desc.logits_row_stride = logits.stride(0)
+    desc.logits = logits.data_ptr()
+    if history is not None and history.shape[1] > 0:
+        desc.history = history.data_ptr()
+        desc.history_row_stride = history.stride(0)
+        desc.hist_len = history.shape[1]
+        desc.history_lens = _device_ptr(history_lens)
+    desc.uniforms = _device_ptr(uniforms)
+    desc.temperature = temperature
+    desc.repetition_penalty = repetition_penalty
+    desc.presence_penalty = presence_penalty
+    desc.frequency_penalty = frequency_penalty
+    desc.top_k = top_k
+    desc.top_p = top_p
+    desc.min_p = min_p
+    desc.greedy = 1 if greedy else 0
+    desc.out_ids = ids.data_ptr()
+    desc.out_logprob = lps.data_ptr()
+    desc.out_kept = kept.data_ptr()
+    desc.out_status = status.data_ptr()
+    lib = _lib.load()
+    ws_bytes = lib.dsv41_sampler_workspace_bytes(_lib.ctypes.byref(desc))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_run(_lib.ctypes.byref(desc), _device_ptr(workspace), ws_bytes, stream)
+    _lib.check(rc)
+    if check:
+        if bool((status != 0).any()):
+            _status_error(status)
+    return SampleResult(ids, lps, kept, status)
+
+
+def sample_next(logits: torch.Tensor, temperature: float,
+                generator: Optional[torch.Generator] = None, **knobs) -> tuple[int, float]:
+    """Drop-in for rollout.py:144-150 on one ``[V]`` (or ``[1, V]``) logits row.
+
+    Returns ``(token, behavior_log_prob)`` like the reference's ``token`` /
+    ``float(log_probs[token])``; the uniform comes from ``torch.rand(1, generator=generator)``.
+    """
+    row = logits.reshape(1, -1) if logits.ndim == 1 else logits
+    if row.ndim != 2 or row.shape[0] != 1:
+        raise ValueError("model next_token_logits must return [1, vocabulary_size]")
+    result = sample(row, temperature=temperature, generator=generator, **knobs)
+    return int(result.ids.item()), float(result.logprobs.item())
