@@ -1,0 +1,221 @@
+"""Benchmark of the MI355X sampler and fused selected-token log-prob (one GPU).
+
+Default line (the driver's N=1 run): config E, the sort-heavy large-batch sampler
+(4096 rows x vocab 151936 fp32, history 4096, T 0.6, repetition 1.05, top-k 1024,
+top-p 0.98, min-p 0.05), plus a ``logprob`` object for config D (16384 tokens x hidden
+7168 -> vocab 129280 with the Token-TIS ratio) when that kernel is built.
+
+A step is one launch over one batch with inputs already resident in HBM.  Times come
+from HIP events on the stream the kernels are launched on, over K back-to-back steps.
+The roofline ``achieved`` figure is algorithmic bytes (sampler) or FLOPs (log-prob)
+per launch over the measured average launch time:
+  sampler bytes/row = V*sizeof(logit) + L_hist*8 + 4 (u) + 8 (id) + 4 (lp) + 4 (kept)
+  log-prob FLOPs/token = 2*H*V
+``cpu_baseline`` times the C oracle (a port of the same specification) on the host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "tiny-dsv41_amd"), str(ROOT)]
+
+METRIC = "sampler rows/s @V=151936; fused logprob tok/s @H=7168; % of HBM/MFMA peak"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by
+# the same counters on a plain copy of known size (profiles/*_traffic.md).  None = not
+# measured for the current kernel build.
+MEASURED_TRAFFIC = {}
+
+
+def sampler_bytes_per_row(vocab, esize, hist_len):
+    return vocab * esize + hist_len * 8 + 4 + 8 + 4 + 4
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="E", choices=["A", "B", "E"])
+    ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
+    ap.add_argument("--logprob-steps", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="time a plain device copy of this many bytes (PMC calibration) and exit")
+    return ap.parse_args()
+
+
+def events_time(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def copy_calibration(nbytes, steps, torch):
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    ms = events_time(lambda: dst.copy_(src), steps, 2, torch)
+    print(json.dumps({"copy_bytes": nbytes, "ms": ms, "GBps": 2 * nbytes / ms / 1e6}), flush=True)
+
+
+def bench_sampler(name, steps, warmup, cpu_baseline, torch):
+    from dsv41_rocm import _lib, workloads
+
+    cfg = workloads.SAMPLER_CONFIGS[name]
+    dev = torch.device("cuda:0")
+    print(f"[bench] generating sampler config {name} on the GPU", file=sys.stderr, flush=True)
+    inp = workloads.sampler_inputs(name, device=dev)
+    logits, history, uniforms, knobs = inp["logits"], inp["history"], inp["uniforms"], inp["knobs"]
+    rows, vocab = logits.shape
+    ids = torch.empty(rows, dtype=torch.int64, device=dev)
+    lps = torch.empty(rows, dtype=torch.float32, device=dev)
+    kept = torch.empty(rows, dtype=torch.int32, device=dev)
+    status = torch.empty(rows, dtype=torch.int32, device=dev)
+    d = _lib.SamplerDesc()
+    d.struct_size = ctypes.sizeof(_lib.SamplerDesc)
+    d.rows, d.vocab = rows, vocab
+    d.logits_dtype = _lib.DTYPE_F32 if logits.dtype == torch.float32 else _lib.DTYPE_BF16
+    d.logits_row_stride = logits.stride(0)
+    d.logits = logits.data_ptr()
+    d.history = history.data_ptr()
+    d.history_row_stride = history.stride(0)
+    d.hist_len = history.shape[1]
+    d.uniforms = uniforms.data_ptr()
+    d.temperature = knobs.get("temperature", 1.0)
+    d.repetition_penalty = knobs.get("repetition_penalty", 1.0)
+    d.presence_penalty = knobs.get("presence_penalty", 0.0)
+    d.frequency_penalty = knobs.get("frequency_penalty", 0.0)
+    d.top_k = knobs.get("top_k", 0)
+    d.top_p = knobs.get("top_p", 1.0)
+    d.min_p = knobs.get("min_p", 0.0)
+    d.greedy = 0
+    d.out_ids, d.out_logprob, d.out_kept, d.out_status = (ids.data_ptr(), lps.data_ptr(),
+                                                          kept.data_ptr(), status.data_ptr())
+    lib = _lib.load()
+    ws_bytes = lib.dsv41_sampler_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        _lib.check(lib.dsv41_sampler_run(ctypes.byref(d), ws.data_ptr(), ws_bytes, stream))
+
+    ms = events_time(step, steps, warmup, torch)
+    assert int(status.max().item()) == 0, "sampler reported a bad row"
+    esize = logits.element_size()
+    per_row = sampler_bytes_per_row(vocab, esize, history.shape[1])
+    achieved = per_row * rows / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": rows / (ms * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if esize == 4 else "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{name}: sampler {rows}x{vocab} "
+                               f"{'fp32' if esize == 4 else 'bf16'}, history {history.shape[1]}",
+                   "rows": rows, "vocab": vocab, "hist_len": history.shape[1], **knobs},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": MEASURED_TRAFFIC.get(f"sampler_{name}"),
+                     "bytes_per_row": per_row},
+    }
+    if cpu_baseline:
+        line["cpu_baseline"] = cpu_sampler_baseline(inp, knobs, torch)
+    return line
+
+
+def cpu_sampler_baseline(inp, knobs, torch):
+    """C oracle (port of the same spec), one thread, on a bounded row sample of the batch;
+    plus the reference's full-vocab expression (rollout.py:144-148) for context."""
+    import numpy as np
+
+    import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    sample_rows = min(inp["logits"].shape[0], 512)
+    x = inp["logits"][:sample_rows].float().cpu().numpy()
+    h = inp["history"][:sample_rows].cpu().numpy()
+    u = inp["uniforms"][:sample_rows].cpu().numpy()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        oracle.sample(x, uniforms=u, history=h, **knobs)
+        n += sample_rows
+        if time.perf_counter() - t0 > 10.0:
+            break
+    dt = time.perf_counter() - t0
+    out = {"value": n / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+           "sample": f"C oracle over the first {sample_rows} rows of the batch, repeated for "
+                     f"{dt:.1f} s on 1 of {cores} host cores"}
+    # reference expression, full-vocab (no penalties/truncation exist in the reference)
+    xt = torch.from_numpy(x[:64])
+    T = knobs.get("temperature", 1.0)
+    g = torch.Generator().manual_seed(0)
+    ref = {}
+    for threads in (1, cores):
+        torch.set_num_threads(threads)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 3.0:
+            for r in range(xt.shape[0]):
+                lp = torch.log_softmax(xt[r] / T, dim=-1)
+                p = lp.exp()
+                tok = int(torch.multinomial(p, 1, generator=g).item())
+                float(lp[tok])
+            reps += xt.shape[0]
+        ref[f"threads_{threads}"] = reps / (time.perf_counter() - t0)
+    out["reference_expression_rows_per_s"] = ref
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (rows and tokens are "
+              "independent, see DESIGN.md for how the path shards)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if args.copy_bytes:
+        copy_calibration(args.copy_bytes, args.steps, torch)
+        return
+    line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
+    if args.logprob != "none":
+        try:
+            from dsv41_rocm import logprob as _lp  # noqa: F401
+        except ImportError:
+            _lp = None
+        if _lp is not None:
+            line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, torch)
+    print(json.dumps(line), flush=True)
+
+
+def bench_logprob(name, steps, warmup, torch):
+    raise NotImplementedError
+
+
+if __name__ == "__main__":
+    main()

@@ -7,23 +7,25 @@
 // [rows, vocab] batch, with the vLLM SamplingParams knobs of
 // rollout_manager/backends/vllm_actor.py:178-185 applied in vLLM v1's order.
 //
-// One workgroup per row streams the row from HBM exactly once:
+// One workgroup per row streams the row from HBM exactly once, through raw buffer
+// loads (out-of-range lanes read 0, so the pipeline has no branches around loads),
+// double-buffered in batches of PF tiles:
 //   FULL    (no truncation): per-chunk (max, sum exp) in LDS, float inverse CDF over
 //           chunk sums, then one 64*G-element chunk is re-read to place the draw.
-//   TOPK    (1 <= top_k <= 4096): elements above a running threshold (top-k of what
-//           has been seen, and the min-p bound from the running max) go to an LDS
+//   TOPK    (1 <= top_k <= 2048): elements above a running threshold (top-k of what
+//           has been seen, and the min-p bound of the running maximum) go to an LDS
 //           candidate buffer; after the pass the buffer is sorted and every decision
 //           (min-p, top-k, top-p, draw) is an exact scan over it.
 //   GENERIC (anything else that truncates): z is written to a workspace row and the
 //           same decisions are made by exact radix selection over it.
+// History tokens are masked out of the stream and re-read per batch from the lines
+// the batch has just brought on chip, then penalized exactly.
 // Selection arithmetic is exact (fp32 compares, fp64 differences of fp32 values,
 // 64-bit fixed-point masses), so kept sets and ids do not depend on reduction order.
 // This file is compiled with -ffp-contract=off: each operation rounds as written.
 
 #include <math.h>
 #include <string.h>
-
-#include <mutex>
 
 #include "common.h"
 
@@ -34,21 +36,28 @@ constexpr int MODE_FULL = 0;
 constexpr int MODE_TOPK = 1;
 constexpr int MODE_GENERIC = 2;
 
-constexpr int NT = 1024;          // threads per workgroup (16 waves)
-constexpr int NW = NT / 64;
-constexpr int TOPK_G = 4;         // elements per thread per tile in TOPK mode
-constexpr int TOPK_TILE = NT * TOPK_G;
-constexpr int TOPK_CAP = 8192;    // candidate buffer entries (u64 keys)
-constexpr int KCAP = TOPK_CAP - TOPK_TILE;  // largest top_k on the one-pass path
-constexpr int MAX_VOCAB = 1 << 21;          // 2^21 * 2^43 < 2^64: mass sums cannot wrap
+constexpr int FULL_NT = 1024;
+constexpr int TOPK_NT = 512;
+constexpr int GEN_NT = 1024;
+constexpr int MAX_NW = 16;
+constexpr int PF = 4;                          // tiles per pipelined batch
+constexpr int TOPK_G = 4;                      // elements per thread per TOPK tile
+constexpr int TOPK_TILE = TOPK_NT * TOPK_G;    // 2048
+constexpr int KCAP = TOPK_TILE;                // largest top_k on the one-pass path
+constexpr int MAX_VOCAB = 1 << 21;             // 2^21 * 2^43 < 2^64: mass sums cannot wrap
+constexpr int MAX_UNIQUE = 65535;              // history slots and counts are 16-bit
 constexpr size_t LDS_LIMIT = 160 * 1024;
 
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr uint32_t NEG_INF_BITS = 0xFF800000u;
 constexpr float LOG2E = 1.4426950408889634f;
 
 constexpr int ST_NONFINITE = DSV41_STATUS_NONFINITE;
 constexpr int ST_BAD_HISTORY = DSV41_STATUS_BAD_HISTORY;
 constexpr int ST_BAD_UNIFORM = DSV41_STATUS_BAD_UNIFORM;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 struct Params {
   const void* logits;
@@ -63,17 +72,18 @@ struct Params {
   int32_t* out_status;
   float* zbuf;
   double log_min_p;
-  float T, rT, rp, pres, freq, top_p, min_p;
-  int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words;
+  float T, rT, rp, pres, freq, top_p, min_p, lmin_f;
+  int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words, cap;
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
 struct Misc {
-  double rd[NW];
-  uint64_t ru[NW];
-  float rf[NW];
-  float wmax[NW];
-  int ri[NW];
+  double rd[MAX_NW];
+  uint64_t ru[MAX_NW];
+  float rf[MAX_NW];
+  float wmax[2][MAX_NW];
+  int ri[MAX_NW];
+  int wcnt[2][MAX_NW];
   uint64_t bu[4];
   double bd[4];
   float bf[4];
@@ -86,7 +96,7 @@ struct Misc {
 };
 
 struct Layout {
-  size_t misc, bitmap, wrank, cnt, penx, hist256, mode0, total;
+  size_t misc, bitmap, wrank, cnt, tok, penx, hist256, mode0, total;
 };
 
 __host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -97,8 +107,10 @@ __host__ __device__ inline int n_chunks(int V) {
 }
 
 // LDS layout; must agree between the launch (host) and the kernel (device).
+// bitmap u32[words] | wrank u16[words] | cnt u16[ucap] | tok u32[ucap] |
+// penx f32[ucap] (FULL) | 256 u64 radix bins | chunks (FULL) or candidates (TOPK)
 template <int MODE, int G>
-__host__ __device__ inline Layout make_layout(int V, int words, int ucap) {
+__host__ __device__ inline Layout make_layout(int V, int words, int ucap, int cap) {
   Layout l;
   size_t off = 0;
   l.misc = off;
@@ -106,16 +118,18 @@ __host__ __device__ inline Layout make_layout(int V, int words, int ucap) {
   l.bitmap = off;
   off += 4 * (size_t)words;
   l.wrank = off;
-  off += 4 * (size_t)words;
+  off = align16(off + 2 * (size_t)words);
   l.cnt = off;
-  off += 4 * (size_t)ucap;
-  l.penx = off;
+  off = align16(off + 2 * (size_t)((ucap + 1) & ~1));
+  l.tok = off;
   off = align16(off + 4 * (size_t)ucap);
+  l.penx = off;
+  if (MODE == MODE_FULL) off = align16(off + 4 * (size_t)ucap);
   l.hist256 = off;
   off += 256 * 8;
   l.mode0 = off;
   if (MODE == MODE_FULL) off += 8 * (size_t)n_chunks<G>(V);
-  if (MODE == MODE_TOPK) off += 8 * (size_t)TOPK_CAP;
+  if (MODE == MODE_TOPK) off += 8 * (size_t)cap;
   l.total = align16(off);
   return l;
 }
@@ -208,7 +222,9 @@ __device__ __forceinline__ bool minp_ok(float z, float zmax, const Params& p) {
 }
 
 // ------------------------------------------------------------ block reductions
+template <int NT>
 __device__ __forceinline__ float block_max(float v, Misc* m) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   v = wave_max(v);
   if (lane == 0) m->rf[wid] = v;
@@ -218,7 +234,9 @@ __device__ __forceinline__ float block_max(float v, Misc* m) {
   __syncthreads();
   return r;
 }
+template <int NT>
 __device__ __forceinline__ int block_sum_i(int v, Misc* m) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   v = wave_sum_i(v);
   if (lane == 0) m->ri[wid] = v;
@@ -228,7 +246,9 @@ __device__ __forceinline__ int block_sum_i(int v, Misc* m) {
   __syncthreads();
   return r;
 }
+template <int NT>
 __device__ __forceinline__ int block_min_i(int v, Misc* m) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   v = wave_min_i(v);
   if (lane == 0) m->ri[wid] = v;
@@ -238,7 +258,9 @@ __device__ __forceinline__ int block_min_i(int v, Misc* m) {
   __syncthreads();
   return r;
 }
+template <int NT>
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, Misc* m) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   v = wave_sum_u64(v);
   if (lane == 0) m->ru[wid] = v;
@@ -248,7 +270,9 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, Misc* m) {
   __syncthreads();
   return r;
 }
+template <int NT>
 __device__ __forceinline__ double block_sum_d(double v, Misc* m) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   v = wave_sum_d(v);
   if (lane == 0) m->rd[wid] = v;
@@ -259,8 +283,9 @@ __device__ __forceinline__ double block_sum_d(double v, Misc* m) {
   return r;
 }
 
-// In-place inclusive prefix sum of a[0..n), n <= 4 * NT.
-__device__ void block_incl_scan_u64(uint64_t* a, int n, Misc* m) {
+// In-place inclusive prefix sum of a[0..n).
+template <int NT>
+__device__ __forceinline__ void block_incl_scan_u64(uint64_t* a, int n, Misc* m) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int per = (n + NT - 1) / NT;
   const int b = tid * per, e = min(b + per, n);
@@ -279,23 +304,40 @@ __device__ void block_incl_scan_u64(uint64_t* a, int n, Misc* m) {
   __syncthreads();
 }
 
-// Descending bitonic sort of a[0..n) (u64 keys), padding to a power of two with 0.
-__device__ void bitonic_sort_desc(uint64_t* a, int n) {
+// Descending sort of a[0..n) (u64 keys) by the bitonic network in its one-direction
+// form (each merge starts with a mirror step, then half-cleaners; every comparator
+// puts the larger key at the lower index).  Positions >= n act as keys below every
+// real key and are never touched, so n need not be a power of two.
+template <int NT>
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t* a, int n) {
   const int tid = threadIdx.x;
-  int P = 2;
+  int P = 1;
   while (P < n) P <<= 1;
-  for (int i = n + tid; i < P; i += NT) a[i] = 0;
-  __syncthreads();
   for (int k = 2; k <= P; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
+    // mirror step inside each k-block
+    for (int i = tid; i < (P >> 1); i += NT) {
+      const int half = k >> 1;
+      const int blk = i / half, off = i - blk * half;
+      const int lo = blk * k + off, hi = blk * k + (k - 1 - off);
+      if (hi < n) {
+        const uint64_t x = a[lo], y = a[hi];
+        if (x < y) {
+          a[lo] = y;
+          a[hi] = x;
+        }
+      }
+    }
+    __syncthreads();
+    for (int j = k >> 2; j > 0; j >>= 1) {
       for (int i = tid; i < (P >> 1); i += NT) {
         const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
         const int hi = lo + j;
-        const bool desc = (lo & k) == 0;
-        const uint64_t x = a[lo], y = a[hi];
-        if ((x < y) == desc) {
-          a[lo] = y;
-          a[hi] = x;
+        if (hi < n) {
+          const uint64_t x = a[lo], y = a[hi];
+          if (x < y) {
+            a[lo] = y;
+            a[hi] = x;
+          }
         }
       }
       __syncthreads();
@@ -308,8 +350,8 @@ __device__ void bitonic_sort_desc(uint64_t* a, int n) {
 // cumulative weight, taken in descending (DESC) or ascending key order, first reaches
 // `target` (>= 1).  Keys must be unique; weight-0 elements are never chosen.  Returns
 // the key, or 0 with *found = false when the total weight is below target.
-template <bool DESC, int NBITS, class Visit>
-__device__ uint64_t radix_select(Visit visit, uint64_t target, uint64_t* hist, Misc* m,
+template <int NT, bool DESC, int NBITS, class Visit>
+__device__ __forceinline__ uint64_t radix_select(Visit visit, uint64_t target, uint64_t* hist, Misc* m,
                                  bool* found) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   uint64_t prefix = 0, mask = 0;
@@ -318,11 +360,11 @@ __device__ uint64_t radix_select(Visit visit, uint64_t target, uint64_t* hist, M
     for (int i = tid; i < 256; i += NT) hist[i] = 0;
     __syncthreads();
     visit([&](uint64_t key, uint64_t w) {
-      if (w != 0 && (key & mask) == prefix) atomicAdd((unsigned long long*)&hist[(key >> shift) & 255], (unsigned long long)w);
+      if (w != 0 && (key & mask) == prefix)
+        atomicAdd((unsigned long long*)&hist[(key >> shift) & 255], (unsigned long long)w);
     });
     __syncthreads();
     if (wid == 0) {
-      // lane l owns 4 bins in traversal order
       uint64_t v[4];
       uint64_t s = 0;
 #pragma unroll
@@ -334,8 +376,7 @@ __device__ uint64_t radix_select(Visit visit, uint64_t target, uint64_t* hist, M
       const uint64_t incl = wave_incl_scan_u64(s, lane);
       const uint64_t before = incl - s;
       const uint64_t total = __shfl(incl, 63);
-      const bool mine = before < target && target <= incl;
-      if (mine) {
+      if (before < target && target <= incl) {
         uint64_t acc = before;
         int digit = 0;
         uint64_t rem = 0;
@@ -371,35 +412,93 @@ __device__ uint64_t radix_select(Visit visit, uint64_t target, uint64_t* hist, M
   return ok ? prefix : 0;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
+  // gfx9 raw buffer: stride 0, num_records = bytes; reads past it return 0
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // ------------------------------------------------------------ history tables
 // bitmap[w] bit b set <=> token 32w+b occurs in the row's history;
-// wrank[w] = number of set bits before word w (slot of the word's first token);
-// cnt[slot] = occurrences.  Returns the number of distinct tokens.
-__device__ int build_history(const Params& p, int row, uint32_t* bitmap, uint32_t* wrank,
-                             uint32_t* cnt, Misc* m) {
+// wrank[w] = number of set bits before word w, so token t has slot
+// wrank[t>>5] + popcount(bitmap[t>>5] below bit t&31); cnt[slot] = occurrences
+// (16-bit halves of u32 words), tok[slot] = token.
+struct Hist {
+  uint32_t* bitmap;
+  uint16_t* wrank;
+  uint32_t* cnt2;
+  uint32_t* tok;
+};
+
+__device__ __forceinline__ int slot_of(const Hist& h, int t) {
+  const uint32_t w = h.bitmap[t >> 5];
+  return (int)h.wrank[t >> 5] + __popc(w & ((1u << (t & 31)) - 1u));
+}
+__device__ __forceinline__ uint32_t count_of(const Hist& h, int s) {
+  return (h.cnt2[s >> 1] >> ((s & 1) * 16)) & 0xFFFFu;
+}
+// number of slots of tokens < e (0 <= e <= V)
+__device__ __forceinline__ int rank_below(const Hist& h, int e, int words, int U) {
+  const int w = e >> 5;
+  if (w >= words) return U;
+  return (int)h.wrank[w] + __popc(h.bitmap[w] & ((1u << (e & 31)) - 1u));
+}
+
+// History ids of one row, loaded into registers at kernel start so that the table
+// build does not wait on memory twice; ids past HR*NT are read again from memory.
+template <int HR>
+struct HistIds {
+  int64_t id[HR];
+  int hl;
+};
+
+template <int NT, int HR>
+__device__ __forceinline__ void load_history(const Params& p, int row, HistIds<HR>& hi) {
+  hi.hl = 0;
+  if (!p.has_pen) return;
+  const int tid = threadIdx.x;
+  const int64_t* hr = p.hist + (int64_t)row * p.hstride;
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(hr, (uint32_t)p.hstride * 8u);
+#pragma unroll
+  for (int j = 0; j < HR; ++j) {
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(tid + j * NT) * 8u, 0, 0);
+    hi.id[j] = (int64_t)(((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x);
+  }
+  int hl = p.hlens ? p.hlens[row] : p.hlen;
+  hi.hl = max(0, min(hl, (int)p.hstride));
+}
+
+// Builds the tables; returns the number of slots (distinct in-vocabulary ids).
+template <int NT, int HR>
+__device__ __forceinline__ int build_history(const Params& p, int row, const HistIds<HR>& hi, const Hist& h, Misc* m) {
+  constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int W = p.words;
-  for (int i = tid; i < W; i += NT) bitmap[i] = 0;
-  for (int i = tid; i < p.ucap; i += NT) cnt[i] = 0;
+  for (int i = tid; i < W; i += NT) h.bitmap[i] = 0;
+  for (int i = tid; i < (p.ucap + 1) / 2; i += NT) h.cnt2[i] = 0;
   __syncthreads();
-  int hl = p.hlens ? p.hlens[row] : p.hlen;
-  hl = max(0, min(hl, (int)p.hstride));
-  const int64_t* h = p.hist + (int64_t)row * p.hstride;
+  const int hl = hi.hl;
+  const int64_t* hr = p.hist + (int64_t)row * p.hstride;
   int bad = 0;
-  for (int j = tid; j < hl; j += NT) {
-    const int64_t id = h[j];
-    if (id >= 0 && id < p.V)
-      atomicOr(&bitmap[id >> 5], 1u << (id & 31));
-    else if (id >= p.V)
-      bad = 1;
+#pragma unroll
+  for (int j = 0; j < HR; ++j) {
+    const int idx = tid + j * NT;
+    if (idx < hl) {
+      const int64_t id = hi.id[j];
+      if (id >= 0 && id < p.V) atomicOr(&h.bitmap[id >> 5], 1u << (id & 31));
+      else if (id >= p.V) bad = 1;
+    }
+  }
+  for (int idx = tid + HR * NT; idx < hl; idx += NT) {
+    const int64_t id = hr[idx];
+    if (id >= 0 && id < p.V) atomicOr(&h.bitmap[id >> 5], 1u << (id & 31));
+    else if (id >= p.V) bad = 1;
   }
   if (bad) atomicOr(&m->status, ST_BAD_HISTORY);
   __syncthreads();
-  // exclusive prefix popcount over words
   const int per = (W + NT - 1) / NT;
   const int b = tid * per, e = min(b + per, W);
   int s = 0;
-  for (int i = b; i < e; ++i) s += __popc(bitmap[i]);
+  for (int i = b; i < e; ++i) s += __popc(h.bitmap[i]);
   const int incl = wave_incl_scan_i(s, lane);
   if (lane == 63) m->ri[wid] = incl;
   __syncthreads();
@@ -407,45 +506,28 @@ __device__ int build_history(const Params& p, int row, uint32_t* bitmap, uint32_
   for (int i = 0; i < wid; ++i) off += m->ri[i];
   int run = off + incl - s;
   for (int i = b; i < e; ++i) {
-    wrank[i] = (uint32_t)run;
-    run += __popc(bitmap[i]);
+    h.wrank[i] = (uint16_t)run;
+    run += __popc(h.bitmap[i]);
   }
   int U = 0;
   for (int i = 0; i < NW; ++i) U += m->ri[i];
   __syncthreads();
-  for (int j = tid; j < hl; j += NT) {
-    const int64_t id = h[j];
+  auto count_id = [&](int64_t id) {
     if (id >= 0 && id < p.V) {
-      const uint32_t w = (uint32_t)(id >> 5), bit = (uint32_t)(id & 31);
-      const uint32_t slot = wrank[w] + __popc(bitmap[w] & ((1u << bit) - 1u));
-      atomicAdd(&cnt[slot], 1u);
+      const int slot = slot_of(h, (int)id);
+      atomicAdd(&h.cnt2[slot >> 1], 1u << ((slot & 1) * 16));
+      h.tok[slot] = (uint32_t)id;
     }
-  }
+  };
+#pragma unroll
+  for (int j = 0; j < HR; ++j)
+    if (tid + j * NT < hl) count_id(hi.id[j]);
+  for (int idx = tid + HR * NT; idx < hl; idx += NT) count_id(hr[idx]);
   __syncthreads();
   return U;
 }
 
-// Token id of history slot s (the s-th set bit of the bitmap).
-__device__ int slot_token(int s, const uint32_t* bitmap, const uint32_t* wrank, int W) {
-  int lo = 0, hi = W - 1;  // largest w with wrank[w] <= s
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if ((int)wrank[mid] <= s) lo = mid;
-    else hi = mid - 1;
-  }
-  uint32_t word = bitmap[lo];
-  for (int k = s - (int)wrank[lo]; k > 0; --k) word &= word - 1u;
-  return lo * 32 + (__ffs(word) - 1);
-}
-
-// Processed logit of history slot s from its captured raw logit penx[s].
-__device__ __forceinline__ float slot_z(int s, const uint32_t* cnt, const float* penx,
-                                        const Params& p) {
-  const float x = penalize(penx[s], cnt[s], p);
-  return x / p.T;
-}
-
-// ------------------------------------------------------------ streaming
+// ------------------------------------------------------------ streaming loads
 template <typename TIn, int G>
 struct Raw {
   static constexpr int WORDS = G * (int)sizeof(TIn) / 4;
@@ -453,41 +535,38 @@ struct Raw {
 };
 
 template <typename TIn, int G, bool VEC>
-__device__ __forceinline__ void load_raw(const TIn* row, int base, int V, Raw<TIn, G>& r) {
+__device__ __forceinline__ void load_group(Raw<TIn, G>& r, __amdgpu_buffer_rsrc_t rs, int base) {
   constexpr int WORDS = Raw<TIn, G>::WORDS;
-  if (VEC && base + G <= V) {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(row + base);
-    if constexpr (WORDS == 4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(src);
-      r.w[0] = v.x;
-      r.w[1] = v.y;
-      r.w[2] = v.z;
-      r.w[3] = v.w;
-    } else if constexpr (WORDS == 2) {
-      const uint2 v = *reinterpret_cast<const uint2*>(src);
-      r.w[0] = v.x;
-      r.w[1] = v.y;
-    } else {
+  const uint32_t off = (uint32_t)base * (uint32_t)sizeof(TIn);
+  if constexpr (VEC && WORDS == 4) {
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    r.w[0] = (uint32_t)v.x;
+    r.w[1] = (uint32_t)v.y;
+    r.w[2] = (uint32_t)v.z;
+    r.w[3] = (uint32_t)v.w;
+  } else if constexpr (VEC && WORDS == 2) {
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    r.w[0] = (uint32_t)v.x;
+    r.w[1] = (uint32_t)v.y;
+  } else if constexpr (sizeof(TIn) == 4) {
 #pragma unroll
-      for (int i = 0; i < WORDS; ++i) r.w[i] = src[i];
-    }
+    for (int j = 0; j < G; ++j) r.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, off + 4 * j, 0, 0);
   } else {
-    // scalar path: unaligned rows and the ragged tail
 #pragma unroll
-    for (int i = 0; i < WORDS; ++i) r.w[i] = 0;
-    if constexpr (sizeof(TIn) == 4) {
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-        if (base + j < V) r.w[j] = reinterpret_cast<const uint32_t*>(row)[base + j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-        if (base + j < V) {
-          const uint32_t h = reinterpret_cast<const uint16_t*>(row)[base + j];
-          r.w[j >> 1] |= (j & 1) ? (h << 16) : h;
-        }
+    for (int i = 0; i < WORDS; ++i) {
+      const uint32_t lo = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 4 * i, 0, 0);
+      const uint32_t hi = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 4 * i + 2, 0, 0);
+      r.w[i] = lo | (hi << 16);
     }
   }
+}
+
+template <typename TIn>
+__device__ __forceinline__ float load_one(__amdgpu_buffer_rsrc_t rs, int idx) {
+  if constexpr (sizeof(TIn) == 4)
+    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)idx * 4u, 0, 0));
+  else
+    return bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)idx * 2u, 0, 0));
 }
 
 template <typename TIn, int G>
@@ -504,26 +583,15 @@ __device__ __forceinline__ void unpack(const Raw<TIn, G>& r, float (&x)[G]) {
   }
 }
 
-// Turns G raw logits at [base, base+G) into processed z (penalized tokens and the
-// tail become -inf; penalized raw logits are captured into penx[slot]).
-template <int G, bool CAPTURE = true>
-__device__ __forceinline__ void process_group(float (&x)[G], int base, const Params& p,
-                                              const uint32_t* bitmap, const uint32_t* wrank,
-                                              float* penx, float (&z)[G], int& bad) {
+// z for G logits at [base, base+G).  History tokens and (TAIL) indices >= V become
+// -inf; the exact values of history tokens come from the batch gather instead.
+template <int G, bool TAIL>
+__device__ __forceinline__ void make_z(const float (&x)[G], int base, const Params& p,
+                                       const uint32_t* bitmap, float (&z)[G], int& bad) {
   uint32_t pen = 0;
-  if (p.has_pen && base < p.V) {
-    const uint32_t word = bitmap[base >> 5];
-    const uint32_t sh = (uint32_t)base & 31u;
-    pen = (word >> sh) & ((1u << G) - 1u);
-    if (CAPTURE && pen) {
-      const uint32_t r0 = wrank[base >> 5] + __popc(word & ((1u << sh) - 1u));
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-        if ((pen >> j) & 1u) penx[r0 + __popc(pen & ((1u << j) - 1u))] = x[j];
-    }
-  }
-  // 2^-100 <= |x| < 2^100: three-operation division is IEEE-exact there (checked
-  // exhaustively on the host for the oracle); outside it, IEEE division.
+  if (p.has_pen && (!TAIL || base < p.V)) pen = (bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u);
+  // 2^-100 <= |x| < 2^100: the three-operation division is IEEE-exact there (checked
+  // exhaustively on the host); outside it, IEEE division.
   uint32_t lo = 0xFFFFFFFFu, hi = 0;
 #pragma unroll
   for (int j = 0; j < G; ++j) {
@@ -548,17 +616,75 @@ __device__ __forceinline__ void process_group(float (&x)[G], int base, const Par
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       z[j] = x[j] / p.T;
-      if (base + j < p.V && !((pen >> j) & 1u) && !isfinite(z[j])) bad = 1;
+      if ((!TAIL || base + j < p.V) && !((pen >> j) & 1u) && !isfinite(z[j])) bad = 1;
     }
   }
+  if (p.has_pen) {
 #pragma unroll
-  for (int j = 0; j < G; ++j)
-    if (base + j >= p.V || ((pen >> j) & 1u)) z[j] = NEG_INF;
+    for (int j = 0; j < G; ++j) {
+      const uint32_t msk = 0u - ((pen >> j) & 1u);
+      z[j] = __uint_as_float((msk & NEG_INF_BITS) | (~msk & __float_as_uint(z[j])));
+    }
+  }
+  if (TAIL) {
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (base + j >= p.V) z[j] = NEG_INF;
+  }
 }
 
-template <typename TIn>
-__device__ __forceinline__ const TIn* row_ptr(const Params& p, int row) {
-  return reinterpret_cast<const TIn*>(p.logits) + (int64_t)row * p.lstride;
+// exact processed logit of a history token from its raw logit
+__device__ __forceinline__ float pen_z(float x, uint32_t c, const Params& p) {
+  return penalize(x, c, p) / p.T;
+}
+
+// Pipelined row stream.  `setup()` builds the history tables while the first batch
+// is in flight and returns the slot count.  `batch(t0, nt, R, s0, n, gx)` processes
+// tiles [t0, t0+PF) (TILE = NT*G elements each; tiles >= nt read as zeros) from the
+// raw registers R, together with the history slots [s0, s0+n) whose tokens lie in
+// those tiles: thread i holds the raw logit of slot s0+i in gx (for i < NT).
+template <typename TIn, int G, int NT, bool VEC, class Setup, class Batch>
+__device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc_t rs, const Hist& h,
+                                           Setup setup, Batch batch) {
+  constexpr int TILE = NT * G;
+  const int tid = threadIdx.x;
+  const int nt = (p.V + TILE - 1) / TILE;
+  Raw<TIn, G> A[PF], B[PF];
+#pragma unroll
+  for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(A[k], rs, k * TILE + tid * G);
+  const int U = setup();
+  auto gather = [&](int t0, int& s0, int& n) -> float {
+    if (!p.has_pen) {
+      s0 = 0;
+      n = 0;
+      return 0.0f;
+    }
+    s0 = rank_below(h, min(t0 * TILE, p.V), p.words, U);
+    n = rank_below(h, min((t0 + PF) * TILE, p.V), p.words, U) - s0;
+    return tid < n ? load_one<TIn>(rs, (int)h.tok[s0 + tid]) : 0.0f;
+  };
+  int sA, nA, sB = 0, nB = 0;
+  float gA = gather(0, sA, nA), gB = 0.0f;
+  for (int t0 = 0; t0 < nt; t0 += 2 * PF) {
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(B[k], rs, (t0 + PF + k) * TILE + tid * G);
+    gB = gather(t0 + PF, sB, nB);
+    batch(t0, nt, A, sA, nA, gA);
+    if (t0 + PF >= nt) break;
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(A[k], rs, (t0 + 2 * PF + k) * TILE + tid * G);
+    gA = gather(t0 + 2 * PF, sA, nA);
+    batch(t0 + PF, nt, B, sB, nB, gB);
+  }
+}
+
+// Conservative fp32 lower bound of mrun + log(min_p) (lmin_f = log(min_p) rounded
+// down): elements below it can never pass min-p, because the row maximum is at
+// least mrun.  The subtracted margin exceeds both roundings of the float sums.
+__device__ __forceinline__ float minp_bound_f(float mrun, float lmin_f) {
+  if (!(mrun > NEG_INF) || !(lmin_f > NEG_INF)) return NEG_INF;
+  const float t = mrun + lmin_f;
+  return t - __builtin_fmaf(fabsf(t), 0x1p-20f, 0x1p-120f);
 }
 
 __device__ __forceinline__ void write_result(const Params& p, int row, Misc* m, int64_t id,
@@ -586,86 +712,103 @@ __device__ __forceinline__ float row_uniform(const Params& p, int row, Misc* m) 
   return u;
 }
 
+template <typename TIn>
+__device__ __forceinline__ const TIn* row_ptr(const Params& p, int row) {
+  return reinterpret_cast<const TIn*>(p.logits) + (int64_t)row * p.lstride;
+}
+
+__device__ __forceinline__ Hist hist_tables(unsigned char* smem, const Layout& L) {
+  Hist h;
+  h.bitmap = reinterpret_cast<uint32_t*>(smem + L.bitmap);
+  h.wrank = reinterpret_cast<uint16_t*>(smem + L.wrank);
+  h.cnt2 = reinterpret_cast<uint32_t*>(smem + L.cnt);
+  h.tok = reinterpret_cast<uint32_t*>(smem + L.tok);
+  return h;
+}
+
 // ====================================================================== FULL
 // No truncation: kept set = whole vocabulary.  Chunk c = [c*64G, (c+1)*64G) is one
 // wave's span of one tile; its (max, sum exp(z - max)) go to LDS.
 template <typename TIn, int G, bool VEC>
-__global__ __launch_bounds__(NT) void full_kernel(Params p) {
+__global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
+  constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
-  const Layout L = make_layout<MODE_FULL, G>(p.V, p.words, p.ucap);
+  const Layout L = make_layout<MODE_FULL, G>(p.V, p.words, p.ucap, 0);
   Misc* m = reinterpret_cast<Misc*>(smem + L.misc);
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(smem + L.bitmap);
-  uint32_t* wrank = reinterpret_cast<uint32_t*>(smem + L.wrank);
-  uint32_t* cnt = reinterpret_cast<uint32_t*>(smem + L.cnt);
-  float* penx = reinterpret_cast<float*>(smem + L.penx);
+  const Hist h = hist_tables(smem, L);
+  float* penz = reinterpret_cast<float*>(smem + L.penx);
   const int NC = n_chunks<G>(p.V);
   float* cm = reinterpret_cast<float*>(smem + L.mode0);
   float* cs = cm + NC;
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  if (tid == 0) m->status = 0;
-  __syncthreads();
-  int U = 0;
-  if (p.has_pen) U = build_history(p, row, bitmap, wrank, cnt, m);
+  HistIds<HR> hi;
+  load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
   constexpr int TILE = NT * G;
-  const int ntiles = (p.V + TILE - 1) / TILE;
   int bad = 0;
-
-  Raw<TIn, G> r0, r1;
-  load_raw<TIn, G, VEC>(src, tid * G, p.V, r0);
-  if (ntiles > 1) load_raw<TIn, G, VEC>(src, TILE + tid * G, p.V, r1);
-  for (int t = 0; t < ntiles; ++t) {
-    Raw<TIn, G> r2;
-    if (t + 2 < ntiles) load_raw<TIn, G, VEC>(src, (t + 2) * TILE + tid * G, p.V, r2);
-    const int base = t * TILE + tid * G;
-    float x[G], z[G];
-    unpack(r0, x);
-    process_group<G>(x, base, p, bitmap, wrank, penx, z, bad);
-    float mx = z[0];
+  int U = 0;
+  stream_row<TIn, G, NT, VEC>(
+      p, rs, h,
+      [&]() {
+        if (tid == 0) m->status = 0;
+        __syncthreads();
+        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        return U;
+      },
+      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
 #pragma unroll
-    for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
-    mx = wave_max(mx);
-    float s = 0.0f;
-    if (mx > NEG_INF) {
-      const float mb = mx * LOG2E;
+        for (int k = 0; k < PF; ++k) {
+          const int t = t0 + k;
+          if (t < nt) {
+            const int base = t * TILE + tid * G;
+            float x[G], z[G];
+            unpack(R[k], x);
+            if ((t + 1) * TILE <= p.V) make_z<G, false>(x, base, p, h.bitmap, z, bad);
+            else make_z<G, true>(x, base, p, h.bitmap, z, bad);
+            float mx = z[0];
 #pragma unroll
-      for (int j = 0; j < G; ++j) s += exp2f(__builtin_fmaf(z[j], LOG2E, -mb));
-    }
-    s = wave_sum(s);
-    const int c = t * NW + wid;
-    if (lane == 0 && c < NC) {
-      cm[c] = mx;
-      cs[c] = s;
-    }
-    r0 = r1;
-    r1 = r2;
-  }
+            for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
+            mx = wave_max_dpp(mx);
+            float s = 0.0f;
+            if (mx > NEG_INF) {
+              const float mb = mx * LOG2E;
+#pragma unroll
+              for (int j = 0; j < G; ++j) s += exp2f(__builtin_fmaf(z[j], LOG2E, -mb));
+            }
+            s = wave_sum_dpp(s);
+            const int c = t * NW + wid;
+            if (lane == 0 && c < NC) {
+              cm[c] = mx;
+              cs[c] = s;
+            }
+          }
+        }
+        for (int i = tid; i < n; i += NT) {
+          const int s = s0 + i;
+          const float x = i == tid ? gx : load_one<TIn>(rs, (int)h.tok[s]);
+          const float z = pen_z(x, count_of(h, s), p);
+          if (!isfinite(z)) bad = 1;
+          penz[s] = z;
+        }
+      });
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
 
-  // penalized tokens: exact z, written back over the captured raw logits
   float pmax = NEG_INF;
-  for (int s = tid; s < U; s += NT) {
-    const float z = slot_z(s, cnt, penx, p);
-    if (!isfinite(z)) atomicOr(&m->status, ST_NONFINITE);
-    penx[s] = z;
-    pmax = fmaxf(pmax, z);
-  }
+  for (int s = tid; s < U; s += NT) pmax = fmaxf(pmax, penz[s]);
   float cmax = NEG_INF;
   for (int c = tid; c < NC; c += NT) cmax = fmaxf(cmax, cm[c]);
-  const float M = block_max(fmaxf(pmax, cmax), m);  // also orders the penx writes
+  const float M = block_max<NT>(fmaxf(pmax, cmax), m);
 
-  // rescale chunk sums to the row maximum, then add the penalized tokens
+  // rescale chunk sums to the row maximum, then add the history tokens
   for (int c = tid; c < NC; c += NT) cs[c] = cm[c] > NEG_INF ? cs[c] * exp2f((cm[c] - M) * LOG2E) : 0.0f;
   __syncthreads();
-  for (int s = tid; s < U; s += NT) {
-    const int tok = slot_token(s, bitmap, wrank, p.words);
-    atomicAdd(&cs[tok / (64 * G)], exp2f((penx[s] - M) * LOG2E));
-  }
+  for (int s = tid; s < U; s += NT) atomicAdd(&cs[h.tok[s] / (64 * G)], exp2f((penz[s] - M) * LOG2E));
   __syncthreads();
 
-  // total mass and chunk prefix (wave 0, fp64)
+  // total mass and the chunk holding the draw (wave 0, fp64)
   const float u = row_uniform(p, row, m);
   if (wid == 0) {
     const int per = (NC + 63) / 64;
@@ -676,7 +819,6 @@ __global__ __launch_bounds__(NT) void full_kernel(Params p) {
     const double S = __shfl(incl, 63);
     const double t = (double)u * S;
     double before = incl - s;
-    // chunk holding t: the one whose [before, before + cs) contains t
     int cstar = -1;
     double cbefore = 0.0;
     if (before <= t && t < incl) {
@@ -695,17 +837,15 @@ __global__ __launch_bounds__(NT) void full_kernel(Params p) {
         cbefore = t + 1.0;
       }
     }
-    // rounding fallback: the last chunk with positive mass
-    unsigned long long hit = __ballot(cstar >= 0);
+    const unsigned long long hit = __ballot(cstar >= 0);
     if (hit == 0) {
       int last = -1;
       for (int c = b; c < e; ++c)
         if (cs[c] > 0.0f) last = c;
-      int lastmax = last;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) lastmax = max(lastmax, __shfl_xor(lastmax, o));
+      for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o));
       if (lane == 0) {
-        m->bi[0] = lastmax;
+        m->bi[0] = last;
         m->bd[0] = -1.0;  // take the last positive element of that chunk
       }
     } else {
@@ -719,34 +859,47 @@ __global__ __launch_bounds__(NT) void full_kernel(Params p) {
     }
     if (lane == 0) m->bd[1] = S;
   }
-  // first chunk whose maximum is the row maximum (for greedy)
+  // first chunk whose maximum is the row maximum, first history token at it (greedy)
   int cfirst = NC;
   for (int c = tid; c < NC; c += NT)
     if (cm[c] == M) cfirst = min(cfirst, c);
   int pfirst = 0x7FFFFFFF;
   for (int s = tid; s < U; s += NT)
-    if (penx[s] == M) pfirst = min(pfirst, slot_token(s, bitmap, wrank, p.words));
-  cfirst = block_min_i(cfirst, m);
-  pfirst = block_min_i(pfirst, m);  // barriers: m->bi/bd visible after this
+    if (penz[s] == M) pfirst = min(pfirst, (int)h.tok[s]);
+  cfirst = block_min_i<NT>(cfirst, m);
+  pfirst = block_min_i<NT>(pfirst, m);
 
   if (wid == 0) {
     const double S = m->bd[1];
     int64_t tok = 0;
     float ztok = M;
+    // one chunk re-read: z of its elements, history tokens restored from penz
+    auto chunk_z = [&](int c, float(&z)[G]) {
+      const int base = c * 64 * G + lane * G;
+      Raw<TIn, G> r;
+      load_group<TIn, G, VEC>(r, rs, base);
+      float x[G];
+      unpack(r, x);
+      int dummy = 0;
+      make_z<G, true>(x, base, p, h.bitmap, z, dummy);
+      if (p.has_pen) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const int v = base + j;
+          if (v < p.V && ((h.bitmap[v >> 5] >> (v & 31)) & 1u)) z[j] = penz[slot_of(h, v)];
+        }
+      }
+    };
     if (p.greedy) {
       int best = pfirst;
       if (cfirst < NC) {
+        float z[G];
+        chunk_z(cfirst, z);
         const int base = cfirst * 64 * G + lane * G;
-        Raw<TIn, G> r;
-        load_raw<TIn, G, VEC>(src, base, p.V, r);
-        float x[G], z[G];
-        unpack(r, x);
-        int dummy = 0;
-        process_group<G, false>(x, base, p, bitmap, wrank, penx, z, dummy);
         int first = 0x7FFFFFFF;
 #pragma unroll
         for (int j = G - 1; j >= 0; --j)
-          if (z[j] == M) first = base + j;
+          if (z[j] == M && base + j < p.V) first = base + j;
         first = wave_min_i(first);
         best = min(best, first);
       }
@@ -760,23 +913,8 @@ __global__ __launch_bounds__(NT) void full_kernel(Params p) {
       const int cstar = m->bi[0];
       const double need = m->bd[0];
       const int base = cstar * 64 * G + lane * G;
-      Raw<TIn, G> r;
-      load_raw<TIn, G, VEC>(src, base, p.V, r);
-      float x[G], z[G], e[G];
-      unpack(r, x);
-      int dummy = 0;
-      process_group<G, false>(x, base, p, bitmap, wrank, penx, z, dummy);
-      // restore penalized elements of this chunk from their exact z
-      if (p.has_pen) {
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-          const int v = base + j;
-          if (v < p.V) {
-            const uint32_t word = bitmap[v >> 5];
-            if ((word >> (v & 31)) & 1u) z[j] = penx[wrank[v >> 5] + __popc(word & ((1u << (v & 31)) - 1u))];
-          }
-        }
-      }
+      float z[G], e[G];
+      chunk_z(cstar, z);
       double ls = 0.0;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
@@ -803,13 +941,12 @@ __global__ __launch_bounds__(NT) void full_kernel(Params p) {
         for (int o = 32; o > 0; o >>= 1) lp = max(lp, __shfl_xor(lp, o));
         chosen = lp;
       }
-      // z of the chosen element
       float zc = NEG_INF;
 #pragma unroll
       for (int j = 0; j < G; ++j)
         if (base + j == chosen) zc = z[j];
       zc = wave_max(zc);
-      tok = chosen;
+      tok = chosen < 0 ? 0 : chosen;
       ztok = zc;
     }
     if (lane == 0) {
@@ -820,173 +957,243 @@ __global__ __launch_bounds__(NT) void full_kernel(Params p) {
 }
 
 // ====================================================================== TOPK
-// One pass: elements with z above the running threshold go to an LDS buffer of
-// ckeys.  Before each tile the buffer is compacted if it could overflow: sorted,
-// cut to top_k and to the min-p bound of the running maximum.
-__device__ void topk_compact(uint64_t* cand, Misc* m, const Params& p, float mrun) {
+// Keeps the candidate buffer at its top_k and within the min-p bound of mrun (a lower
+// bound of the row maximum); returns the new count and updates tau / tau_key.
+template <int NT>
+__device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, const Params& p, float mrun, float& tau,
+                            uint64_t& tau_key) {
   const int tid = threadIdx.x;
-  const int n = m->count;
-  bitonic_sort_desc(cand, n);
-  int el = 0;
+  bitonic_sort_desc<NT>(cand, n);
+  int el = n;
   if (p.min_p > 0.0f && mrun > NEG_INF) {
-    for (int i = tid; i < n; i += NT) el += minp_ok(ckey_z(cand[i]), mrun, p) ? 1 : 0;
-    el = block_sum_i(el, m);
-  } else {
-    el = n;
+    int e = 0;
+    for (int i = tid; i < n; i += NT) e += minp_ok(ckey_z(cand[i]), mrun, p) ? 1 : 0;
+    el = block_sum_i<NT>(e, m);
   }
   const int keep = min(el, p.top_k);
-  if (tid == 0) {
-    if (keep == p.top_k && keep > 0) {
-      m->tau = ckey_z(cand[keep - 1]);
-      m->tau_key = cand[keep - 1];
-    }
-    m->count = keep;
+  if (keep == p.top_k && keep > 0) {
+    tau_key = cand[keep - 1];
+    tau = ckey_z(tau_key);
   }
   __syncthreads();
-}
-
-__device__ __forceinline__ float minp_bound(float mrun, const Params& p) {
-  if (!(p.min_p > 0.0f) || !(mrun > NEG_INF)) return NEG_INF;
-  // conservative fp32 lower bound of mrun + log(min_p)
-  const double d = (double)mrun + p.log_min_p;
-  const double slack = 1e-6 * (fabs((double)mrun) + fabs(p.log_min_p) + 1.0);
-  return (float)(d - slack);
+  return keep;
 }
 
 template <typename TIn, bool VEC>
-__global__ __launch_bounds__(NT) void topk_kernel(Params p) {
-  constexpr int G = TOPK_G;
+__global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
+  constexpr int NT = TOPK_NT, NW = NT / 64, G = TOPK_G, TILE = TOPK_TILE, HR = 8;
+  constexpr int NE = PF * G + 1;  // elements per thread in one batch round (+1 history slot)
   extern __shared__ __align__(16) unsigned char smem[];
-  const Layout L = make_layout<MODE_TOPK, G>(p.V, p.words, p.ucap);
+  const Layout L = make_layout<MODE_TOPK, G>(p.V, p.words, p.ucap, p.cap);
   Misc* m = reinterpret_cast<Misc*>(smem + L.misc);
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(smem + L.bitmap);
-  uint32_t* wrank = reinterpret_cast<uint32_t*>(smem + L.wrank);
-  uint32_t* cnt = reinterpret_cast<uint32_t*>(smem + L.cnt);
-  float* penx = reinterpret_cast<float*>(smem + L.penx);
+  const Hist h = hist_tables(smem, L);
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + L.hist256);
   uint64_t* cand = reinterpret_cast<uint64_t*>(smem + L.mode0);
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  if (tid == 0) {
-    m->status = 0;
-    m->count = 0;
-    m->tau = NEG_INF;
-    m->tau_key = 0;
-  }
-  if (tid < NW) m->wmax[tid] = NEG_INF;
-  __syncthreads();
-  int U = 0;
-  if (p.has_pen) U = build_history(p, row, bitmap, wrank, cnt, m);
+  HistIds<HR> hi;
+  load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
-  constexpr int TILE = TOPK_TILE;
-  const int ntiles = (p.V + TILE - 1) / TILE;
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
   int bad = 0;
+  int count = 0;            // candidates stored (uniform across the workgroup)
+  float tau = NEG_INF;      // z of the top_k-th candidate once the buffer held top_k
+  uint64_t tau_key = 0;
+  float wm = NEG_INF;       // this wave's running maximum (a lower bound of the row max)
+  float mblk = NEG_INF;     // all waves' running maxima at the last exchange
+  int par = 0;
 
-  Raw<TIn, G> r0, r1, r2;
-  load_raw<TIn, G, VEC>(src, tid * G, p.V, r0);
-  if (ntiles > 1) load_raw<TIn, G, VEC>(src, TILE + tid * G, p.V, r1);
-  if (ntiles > 2) load_raw<TIn, G, VEC>(src, 2 * TILE + tid * G, p.V, r2);
-  for (int t = 0; t < ntiles; ++t) {
-    Raw<TIn, G> r3;
-    if (t + 3 < ntiles) load_raw<TIn, G, VEC>(src, (t + 3) * TILE + tid * G, p.V, r3);
-    const int base = t * TILE + tid * G;
-    float x[G], z[G];
-    unpack(r0, x);
-    process_group<G>(x, base, p, bitmap, wrank, penx, z, bad);
-    float mx = z[0];
-#pragma unroll
-    for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
-    mx = wave_max(mx);
-    if (lane == 0) m->wmax[wid] = fmaxf(m->wmax[wid], mx);
+  // One exchange of per-wave insert counts and running maxima over one barrier; the
+  // buffer is compacted when the round could overflow it.  Returns this wave's first
+  // position, or -1 when the round does not fit even after compaction.
+  auto exchange = [&](uint32_t wn, int& total) -> int {
+    if (lane == 0) {
+      m->wcnt[par][wid] = (int)wn;
+      m->wmax[par][wid] = wm;
+    }
     __syncthreads();
-    float mrun = m->wmax[0];
-    for (int i = 1; i < NW; ++i) mrun = fmaxf(mrun, m->wmax[i]);
-    const int cnow = m->count;
-    __syncthreads();  // every wave has read the count before any inserts
-    if (cnow + TILE > TOPK_CAP) topk_compact(cand, m, p, mrun);
-    const float tau = m->tau;
-    const float tmp = minp_bound(mrun, p);
+    total = 0;
+    int before = 0;
+    float mb = NEG_INF;
+    for (int i = 0; i < NW; ++i) {
+      const int v = m->wcnt[par][i];
+      total += v;
+      if (i < wid) before += v;
+      mb = fmaxf(mb, m->wmax[par][i]);
+    }
+    mblk = mb;
+    par ^= 1;
+    if (count + total > p.cap) count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key);
+    return count + total <= p.cap ? count + before : -1;
+  };
+  // One insertion round of up to M (<= G) elements per thread; always fits, because
+  // after a compaction count <= top_k and cap = top_k + TILE.
+  auto round = [&](auto&& elem, int M) {
+    unsigned long long bal[G];
+    uint32_t wn = 0;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      const bool pred = z[j] > tau && z[j] >= tmp;
-      const unsigned long long bal = __ballot(pred);
-      if (bal) {
-        const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        int pos0 = 0;
-        if (lane == 0) pos0 = atomicAdd(&m->count, (int)__popcll(bal));
-        pos0 = __shfl(pos0, 0);
-        if (pred) cand[pos0 + (int)before] = ckey(z[j], (uint32_t)(base + j));
+      bal[j] = 0;
+      if (j < M) {
+        uint64_t key;
+        bal[j] = __ballot(elem(j, key));
+        wn += (uint32_t)__popcll(bal[j]);
       }
     }
-    r0 = r1;
-    r1 = r2;
-    r2 = r3;
-  }
+    int total;
+    int pos = exchange(wn, total);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < M && bal[j]) {
+        if ((bal[j] >> lane) & 1ull) {
+          uint64_t key;
+          elem(j, key);
+          cand[pos + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[j] >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)bal[j], 0u))] = key;
+        }
+        pos += (int)__popcll(bal[j]);
+      }
+    }
+    count += total;
+  };
+
+  int U = 0;
+  stream_row<TIn, G, NT, VEC>(
+      p, rs, h,
+      [&]() {
+        if (tid == 0) m->status = 0;
+        __syncthreads();
+        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        return U;
+      },
+      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+        float z[PF][G];
+        float lm = NEG_INF;
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+          const int t = t0 + k;
+          if (t < nt) {
+            const int base = t * TILE + tid * G;
+            float x[G];
+            unpack(R[k], x);
+            if ((t + 1) * TILE <= p.V) make_z<G, false>(x, base, p, h.bitmap, z[k], bad);
+            else make_z<G, true>(x, base, p, h.bitmap, z[k], bad);
+          } else {
+#pragma unroll
+            for (int j = 0; j < G; ++j) z[k][j] = NEG_INF;
+          }
+#pragma unroll
+          for (int j = 0; j < G; ++j) lm = fmaxf(lm, z[k][j]);
+        }
+        // the batch's first NT history slots, penalized exactly
+        float zg = NEG_INF;
+        uint32_t tg = 0;
+        if (tid < n) {
+          const int s = s0 + tid;
+          tg = h.tok[s];
+          zg = pen_z(gx, count_of(h, s), p);
+          if (!isfinite(zg)) bad = 1;
+        }
+        lm = fmaxf(lm, zg);
+        wm = fmaxf(wm, wave_max_dpp(lm));
+        const float bnd = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
+        const float th = tau;
+        const uint64_t tk = tau_key;
+        // stream elements: later tiles hold larger indices, so z > tau suffices against
+        // the k-th key; history tokens arrive out of order and compare full keys
+        unsigned long long bal[NE];
+        uint32_t wn = 0;
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+#pragma unroll
+          for (int j = 0; j < G; ++j) {
+            bal[k * G + j] = __ballot(z[k][j] > th && z[k][j] >= bnd);
+            wn += (uint32_t)__popcll(bal[k * G + j]);
+          }
+        const uint64_t kg = ckey(zg, tg);
+        bal[NE - 1] = __ballot(zg > NEG_INF && kg > tk && zg >= bnd);
+        wn += (uint32_t)__popcll(bal[NE - 1]);
+        int total;
+        int pos = exchange(wn, total);
+        if (pos >= 0) {
+#pragma unroll
+          for (int e = 0; e < NE; ++e) {
+            if (bal[e]) {
+              if ((bal[e] >> lane) & 1ull) {
+                const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[e] >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal[e], 0u));
+                const uint64_t key = e == NE - 1 ? kg
+                                                 : ckey(z[e / G][e % G], (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
+                cand[pos + below] = key;
+              }
+              pos += (int)__popcll(bal[e]);
+            }
+          }
+          count += total;
+        } else {
+          // the batch does not fit: one round per tile, then the history round
+#pragma unroll
+          for (int k = 0; k < PF; ++k) {
+            const float th2 = tau;
+            const int base = (t0 + k) * TILE + tid * G;
+            round([&](int j, uint64_t& key) {
+                    key = ckey(z[k][j], (uint32_t)(base + j));
+                    return z[k][j] > th2 && z[k][j] >= bnd;
+                  }, G);
+          }
+          const uint64_t tk2 = tau_key;
+          round([&](int, uint64_t& key) {
+                  key = kg;
+                  return zg > NEG_INF && kg > tk2 && zg >= bnd;
+                }, 1);
+        }
+        // history slots past the first NT of this batch
+        for (int i0 = NT; i0 < n; i0 += NT) {
+          const int i = i0 + tid;
+          float z2 = NEG_INF;
+          uint32_t t2 = 0;
+          if (i < n) {
+            const int s = s0 + i;
+            t2 = h.tok[s];
+            z2 = pen_z(load_one<TIn>(rs, (int)t2), count_of(h, s), p);
+            if (!isfinite(z2)) bad = 1;
+          }
+          wm = fmaxf(wm, wave_max_dpp(z2));
+          const float bnd2 = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
+          const uint64_t k2 = ckey(z2, t2), tk3 = tau_key;
+          round([&](int, uint64_t& key) {
+                  key = k2;
+                  return z2 > NEG_INF && k2 > tk3 && z2 >= bnd2;
+                }, 1);
+        }
+      });
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
 
-  // penalized tokens (arbitrary indices: compare full keys against the k-th key)
-  if (U > 0) {
-    float mrun = m->wmax[0];
-    for (int i = 1; i < NW; ++i) mrun = fmaxf(mrun, m->wmax[i]);
-    float pm = NEG_INF;
-    for (int s = tid; s < U; s += NT) {
-      const float z = slot_z(s, cnt, penx, p);
-      if (!isfinite(z)) atomicOr(&m->status, ST_NONFINITE);
-      penx[s] = z;
-      pm = fmaxf(pm, z);
-    }
-    pm = block_max(pm, m);
-    mrun = fmaxf(mrun, pm);
-    for (int s0 = 0; s0 < U; s0 += NT) {
-      const int cnow = m->count;
-      __syncthreads();
-      if (cnow + NT > TOPK_CAP) topk_compact(cand, m, p, mrun);
-      const uint64_t tk = m->tau_key;
-      const float tmp = minp_bound(mrun, p);
-      const int s = s0 + tid;
-      bool pred = false;
-      uint64_t key = 0;
-      if (s < U) {
-        const float z = penx[s];
-        key = ckey(z, (uint32_t)slot_token(s, bitmap, wrank, p.words));
-        pred = key > tk && z >= tmp && z > NEG_INF;
-      }
-      const unsigned long long bal = __ballot(pred);
-      if (bal) {
-        const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        int pos0 = 0;
-        if (lane == 0) pos0 = atomicAdd(&m->count, (int)__popcll(bal));
-        pos0 = __shfl(pos0, 0);
-        if (pred) cand[pos0 + (int)before] = key;
-      }
-      __syncthreads();
-    }
-  }
-
   // final selection over the candidates
-  const int n = m->count;
-  bitonic_sort_desc(cand, n);
+  const int n = count;
+  bitonic_sort_desc<NT>(cand, n);
   const float u = row_uniform(p, row, m);
-  const float zmax = ckey_z(cand[0]);
-  int el = 0;
-  for (int i = tid; i < n; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
-  el = block_sum_i(el, m);
-  const int K = min(p.top_k, el);
-  if (K == 0) {  // only possible for rows without a finite maximum
+  if (n == 0) {  // only possible for rows without a finite maximum
+    __syncthreads();
     if (tid == 0) {
       m->status |= ST_NONFINITE;
       write_result(p, row, m, -1, 0.0f, 0);
     }
     return;
   }
-  uint64_t* q = cand + TOPK_CAP / 2;  // K <= KCAP = TOPK_CAP / 2 entries, beyond the prefix
+  const float zmax = ckey_z(cand[0]);
+  int el = 0;
+  for (int i = tid; i < n; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
+  el = block_sum_i<NT>(el, m);
+  const int K = min(p.top_k, el);
+  uint64_t* q = cand + K;  // K <= KCAP = TILE and cap = top_k + TILE >= 2K
   for (int i = tid; i < K; i += NT) q[i] = mass_of(ckey_z(cand[i]), zmax);
   __syncthreads();
   int n_keep = K;
   uint64_t S;
   if (p.top_p < 1.0f) {
-    block_incl_scan_u64(q, K, m);
+    block_incl_scan_u64<NT>(q, K, m);
     const uint64_t thr = top_p_threshold(p.top_p, q[K - 1]);
     if (tid == 0) m->bi[1] = K - 1;
     __syncthreads();
@@ -999,11 +1206,11 @@ __global__ __launch_bounds__(NT) void topk_kernel(Params p) {
   } else {
     uint64_t s = 0;
     for (int i = tid; i < K; i += NT) s += q[i];
-    S = block_sum_u64(s, m);
+    S = block_sum_u64<NT>(s, m);
   }
   double es = 0.0;
   for (int i = tid; i < n_keep; i += NT) es += exp_det((double)ckey_z(cand[i]) - (double)zmax);
-  const double esum = block_sum_d(es, m);
+  const double esum = block_sum_d<NT>(es, m);
 
   int64_t tok;
   float ztok;
@@ -1013,7 +1220,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(Params p) {
   } else {
     const uint64_t t = draw_target(u, S);
     bool found = false;
-    const uint64_t idx = radix_select<false, 24>(
+    const uint64_t idx = radix_select<NT, false, 24>(
         [&](auto&& f) {
           for (int i = tid; i < n_keep; i += NT) {
             const uint64_t k = cand[i];
@@ -1037,49 +1244,61 @@ __global__ __launch_bounds__(NT) void topk_kernel(Params p) {
 
 // ====================================================================== GENERIC
 template <typename TIn, int G, bool VEC>
-__global__ __launch_bounds__(NT) void generic_kernel(Params p) {
+__global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
+  constexpr int NT = GEN_NT, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
-  const Layout L = make_layout<MODE_GENERIC, G>(p.V, p.words, p.ucap);
+  const Layout L = make_layout<MODE_GENERIC, G>(p.V, p.words, p.ucap, 0);
   Misc* m = reinterpret_cast<Misc*>(smem + L.misc);
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(smem + L.bitmap);
-  uint32_t* wrank = reinterpret_cast<uint32_t*>(smem + L.wrank);
-  uint32_t* cnt = reinterpret_cast<uint32_t*>(smem + L.cnt);
-  float* penx = reinterpret_cast<float*>(smem + L.penx);
+  const Hist h = hist_tables(smem, L);
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + L.hist256);
 
   const int row = blockIdx.x, tid = threadIdx.x;
-  if (tid == 0) m->status = 0;
-  __syncthreads();
-  int U = 0;
-  if (p.has_pen) U = build_history(p, row, bitmap, wrank, cnt, m);
+  HistIds<HR> hi;
+  load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
   float* zr = p.zbuf + (int64_t)row * p.V;
   constexpr int TILE = NT * G;
-  const int ntiles = (p.V + TILE - 1) / TILE;
   int bad = 0;
-  for (int t = 0; t < ntiles; ++t) {
-    const int base = t * TILE + tid * G;
-    Raw<TIn, G> r;
-    load_raw<TIn, G, VEC>(src, base, p.V, r);
-    float x[G], z[G];
-    unpack(r, x);
-    process_group<G>(x, base, p, bitmap, wrank, penx, z, bad);
+  int U = 0;
+  stream_row<TIn, G, NT, VEC>(
+      p, rs, h,
+      [&]() {
+        if (tid == 0) m->status = 0;
+        __syncthreads();
+        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        return U;
+      },
+      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
 #pragma unroll
-    for (int j = 0; j < G; ++j)
-      if (base + j < p.V) zr[base + j] = z[j];
-  }
+        for (int k = 0; k < PF; ++k) {
+          const int t = t0 + k;
+          if (t < nt) {
+            const int base = t * TILE + tid * G;
+            float x[G], z[G];
+            unpack(R[k], x);
+            make_z<G, true>(x, base, p, h.bitmap, z, bad);
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+              if (base + j < p.V) zr[base + j] = z[j];
+          }
+        }
+        // the tiles wrote -inf at history tokens: order those stores before the exact ones
+        __threadfence_block();
+        __syncthreads();
+        for (int i = tid; i < n; i += NT) {
+          const int s = s0 + i;
+          const float x = i == tid ? gx : load_one<TIn>(rs, (int)h.tok[s]);
+          const float z = pen_z(x, count_of(h, s), p);
+          if (!isfinite(z)) bad = 1;
+          zr[h.tok[s]] = z;
+        }
+      });
   if (bad) atomicOr(&m->status, ST_NONFINITE);
-  __syncthreads();
-  for (int s = tid; s < U; s += NT) {
-    const float z = slot_z(s, cnt, penx, p);
-    if (!isfinite(z)) atomicOr(&m->status, ST_NONFINITE);
-    zr[slot_token(s, bitmap, wrank, p.words)] = z;
-  }
   __threadfence_block();
   __syncthreads();
 
   const int V = p.V;
-  // row maximum and its first index
   float bm = NEG_INF;
   int bi = 0x7FFFFFFF;
   for (int i = tid; i < V; i += NT) {
@@ -1089,19 +1308,19 @@ __global__ __launch_bounds__(NT) void generic_kernel(Params p) {
       bi = i;
     }
   }
-  const float zmax = block_max(bm, m);
-  int am = block_min_i(bm == zmax ? bi : 0x7FFFFFFF, m);
+  const float zmax = block_max<NT>(bm, m);
+  int am = block_min_i<NT>(bm == zmax ? bi : 0x7FFFFFFF, m);
   if (am < 0 || am >= V) am = 0;  // no finite maximum: the row is flagged non-finite
   const float u = row_uniform(p, row, m);
 
   int el = 0;
   for (int i = tid; i < V; i += NT) el += minp_ok(zr[i], zmax, p) ? 1 : 0;
-  el = block_sum_i(el, m);
+  el = block_sum_i<NT>(el, m);
   const int K = (p.top_k > 0 && p.top_k < el) ? p.top_k : el;
   bool found = false;
   uint64_t B1 = 0;
   if (K < el) {
-    B1 = radix_select<true, 64>(
+    B1 = radix_select<NT, true, 64>(
         [&](auto&& f) {
           for (int i = tid; i < V; i += NT) {
             const float z = zr[i];
@@ -1117,9 +1336,9 @@ __global__ __launch_bounds__(NT) void generic_kernel(Params p) {
       const float z = zr[i];
       if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B1) s1 += mass_of(z, zmax);
     }
-    s1 = block_sum_u64(s1, m);
+    s1 = block_sum_u64<NT>(s1, m);
     const uint64_t thr = top_p_threshold(p.top_p, s1);
-    B = radix_select<true, 64>(
+    B = radix_select<NT, true, 64>(
         [&](auto&& f) {
           for (int i = tid; i < V; i += NT) {
             const float z = zr[i];
@@ -1141,13 +1360,13 @@ __global__ __launch_bounds__(NT) void generic_kernel(Params p) {
       es += exp_det((double)z - (double)zmax);
     }
   }
-  nk = block_sum_i(nk, m);
-  sk = block_sum_u64(sk, m);
-  const double esum = block_sum_d(es, m);
+  nk = block_sum_i<NT>(nk, m);
+  sk = block_sum_u64<NT>(sk, m);
+  const double esum = block_sum_d<NT>(es, m);
   int64_t tok = am;
   if (!p.greedy) {
     const uint64_t t = draw_target(u, sk);
-    const uint64_t idx = radix_select<false, 24>(
+    const uint64_t idx = radix_select<NT, false, 24>(
         [&](auto&& f) {
           for (int i = tid; i < V; i += NT) {
             const float z = zr[i];
@@ -1166,10 +1385,10 @@ __global__ __launch_bounds__(NT) void generic_kernel(Params p) {
 
 // ====================================================================== host
 template <class K>
-int launch(K kernel, size_t lds, int rows, const Params& prm, hipStream_t stream) {
+int launch(K kernel, int nt, size_t lds, int rows, const Params& prm, hipStream_t stream) {
   DSV41_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-  hipLaunchKernelGGL(kernel, dim3(rows), dim3(NT), lds, stream, prm);
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT));
+  hipLaunchKernelGGL(kernel, dim3(rows), dim3(nt), lds, stream, prm);
   DSV41_HIP_CHECK(hipGetLastError());
   return DSV41_OK;
 }
@@ -1179,7 +1398,7 @@ struct Plan {
   int esize;
   bool vec;
   bool has_pen;
-  int words, ucap;
+  int words, ucap, cap;
   size_t lds;
   size_t workspace;
 };
@@ -1210,7 +1429,8 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
   const bool pen_on = d->repetition_penalty != 1.0f || d->presence_penalty != 0.0f || d->frequency_penalty != 0.0f;
   const bool hist_given = d->history != nullptr && (d->history_lens != nullptr || d->hist_len > 0);
   if (hist_given) {
-    if (d->history_row_stride <= 0) return fail(DSV41_E_INVALID, "history row stride must be positive");
+    if (d->history_row_stride <= 0 || d->history_row_stride > (1 << 27))
+      return fail(DSV41_E_INVALID, "history row stride must be in [1, 2^27]");
     if (!d->history_lens && (d->hist_len < 0 || d->hist_len > d->history_row_stride))
       return fail(DSV41_E_INVALID, "hist_len must be within the history row stride");
   }
@@ -1224,14 +1444,17 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
   else pl->mode = MODE_GENERIC;
   pl->words = pl->has_pen ? (V + 31) / 32 : 0;
   pl->ucap = pl->has_pen ? (int)std::min<int64_t>(d->history_row_stride, V) : 0;
+  if (pl->ucap > MAX_UNIQUE)
+    return fail(DSV41_E_UNSUPPORTED, "history longer than 65535 ids per row is not supported");
+  pl->cap = pl->mode == MODE_TOPK ? d->top_k + TOPK_TILE : 0;
   Layout L;
   if (pl->mode == MODE_FULL)
-    L = pl->esize == 4 ? make_layout<MODE_FULL, 4>(V, pl->words, pl->ucap)
-                       : make_layout<MODE_FULL, 8>(V, pl->words, pl->ucap);
+    L = pl->esize == 4 ? make_layout<MODE_FULL, 4>(V, pl->words, pl->ucap, 0)
+                       : make_layout<MODE_FULL, 8>(V, pl->words, pl->ucap, 0);
   else if (pl->mode == MODE_TOPK)
-    L = make_layout<MODE_TOPK, TOPK_G>(V, pl->words, pl->ucap);
+    L = make_layout<MODE_TOPK, TOPK_G>(V, pl->words, pl->ucap, pl->cap);
   else
-    L = make_layout<MODE_GENERIC, 4>(V, pl->words, pl->ucap);
+    L = make_layout<MODE_GENERIC, 4>(V, pl->words, pl->ucap, 0);
   pl->lds = L.total;
   if (pl->lds > LDS_LIMIT)
     return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
@@ -1271,6 +1494,12 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   p.out_status = d->out_status;
   p.zbuf = static_cast<float*>(workspace);
   p.log_min_p = d->min_p > 0.0f ? std::log((double)d->min_p) : -INFINITY;
+  {
+    // log(min_p) as a float rounded toward -inf, for the conservative in-stream bound
+    float lf = (float)p.log_min_p;
+    if ((double)lf > p.log_min_p) lf = std::nextafter(lf, -INFINITY);
+    p.lmin_f = d->min_p > 0.0f ? lf : -INFINITY;
+  }
   p.T = d->temperature;
   p.rT = 1.0f / d->temperature;
   p.rp = d->repetition_penalty;
@@ -1290,23 +1519,24 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   p.unit_T = d->temperature == 1.0f ? 1 : 0;
   p.ucap = pl.ucap;
   p.words = pl.words;
+  p.cap = pl.cap;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = pl.esize == 2;
   switch (pl.mode) {
     case MODE_FULL:
-      if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true>, pl.lds, d->rows, p, s)
-                            : launch(full_kernel<uint16_t, 8, false>, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(full_kernel<float, 4, true>, pl.lds, d->rows, p, s)
-                    : launch(full_kernel<float, 4, false>, pl.lds, d->rows, p, s);
+      if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true>, FULL_NT, pl.lds, d->rows, p, s)
+                            : launch(full_kernel<uint16_t, 8, false>, FULL_NT, pl.lds, d->rows, p, s);
+      return pl.vec ? launch(full_kernel<float, 4, true>, FULL_NT, pl.lds, d->rows, p, s)
+                    : launch(full_kernel<float, 4, false>, FULL_NT, pl.lds, d->rows, p, s);
     case MODE_TOPK:
-      if (bf) return pl.vec ? launch(topk_kernel<uint16_t, true>, pl.lds, d->rows, p, s)
-                            : launch(topk_kernel<uint16_t, false>, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(topk_kernel<float, true>, pl.lds, d->rows, p, s)
-                    : launch(topk_kernel<float, false>, pl.lds, d->rows, p, s);
+      if (bf) return pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
+                            : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
+      return pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
+                    : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
     default:
-      if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, pl.lds, d->rows, p, s)
-                            : launch(generic_kernel<uint16_t, 4, false>, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(generic_kernel<float, 4, true>, pl.lds, d->rows, p, s)
-                    : launch(generic_kernel<float, 4, false>, pl.lds, d->rows, p, s);
+      if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
+                            : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, pl.lds, d->rows, p, s);
+      return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
+                    : launch(generic_kernel<float, 4, false>, GEN_NT, pl.lds, d->rows, p, s);
   }
 }
