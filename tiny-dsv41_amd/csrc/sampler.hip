@@ -633,6 +633,56 @@ __device__ __forceinline__ void make_z(const float (&x)[G], int base, const Para
   }
 }
 
+// Raw logits with history tokens and (TAIL) indices >= V set to -inf.  Non-finite
+// raw logits are collected into the wave mask nf; ax tracks the largest |x|.
+template <int G, bool TAIL>
+__device__ __forceinline__ void mask_x(const float (&x)[G], int base, const Params& p,
+                                       const uint32_t* bitmap, float (&xm)[G], unsigned long long& nf,
+                                       float& ax) {
+  uint32_t pen = 0;
+  if (p.has_pen && (!TAIL || base < p.V)) pen = (bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u);
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    nf |= __ballot(!isfinite(x[j]));  // positions >= V read as 0 and never count
+    ax = fmaxf(ax, fabsf(x[j]));
+    const uint32_t msk = 0u - ((pen >> j) & 1u);
+    xm[j] = __uint_as_float((msk & NEG_INF_BITS) | (~msk & __float_as_uint(x[j])));
+    if (TAIL && base + j >= p.V) xm[j] = NEG_INF;
+  }
+}
+
+// Adjacent floats (IEEE order; -0 is treated as +0; infinities and NaN map to themselves
+// where no neighbour exists).
+__device__ __forceinline__ float next_up(float x) {
+  if (x != x) return x;
+  uint32_t b = __float_as_uint(x);
+  if (b == 0x80000000u) b = 0;
+  if ((int32_t)b >= 0) {
+    if (b == 0x7F800000u) return x;
+    return __uint_as_float(b + 1u);
+  }
+  return __uint_as_float(b - 1u);
+}
+__device__ __forceinline__ float next_down(float x) { return -next_up(-x); }
+
+// Smallest float x with RN(x / T) > t.  RN(x / T) is non-decreasing in x, so these x
+// form an up-set; its least element is reached by stepping from t*T.  If the steps
+// run out the result errs low, which only admits more candidates.
+__device__ __forceinline__ float x_above(float t, const Params& p) {
+  if (!(t > NEG_INF)) return -__FLT_MAX__;
+  if (!(t < __builtin_huge_valf())) return __builtin_huge_valf();
+  float x = t * p.T;
+  for (int i = 0; i < 8 && x / p.T > t; ++i) x = next_down(x);
+  if (x / p.T > t) x = x - __builtin_fmaf(fabsf(x), 0x1p-10f, 0x1p-126f);
+  for (int i = 0; i < 8 && !(x / p.T > t); ++i) x = next_up(x);
+  return x;
+}
+
+// Raw-logit threshold of the TOPK filter: x passes iff RN(x/T) > tau and RN(x/T) >= bnd.
+__device__ __forceinline__ float x_threshold(float tau, float bnd, const Params& p) {
+  return fmaxf(x_above(tau, p), x_above(next_down(bnd), p));
+}
+
 // exact processed logit of a history token from its raw logit
 __device__ __forceinline__ float pen_z(float x, uint32_t c, const Params& p) {
   return penalize(x, c, p) / p.T;
@@ -1002,6 +1052,9 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   float wm = NEG_INF;       // this wave's running maximum (a lower bound of the row max)
   float mblk = NEG_INF;     // all waves' running maxima at the last exchange
   int par = 0;
+  unsigned long long nfx = 0;  // lanes that saw a non-finite raw logit
+  float ax = 0.0f;             // largest |x| seen by this lane
+  float c_tau = __builtin_nanf(""), c_bnd = __builtin_nanf(""), c_thr = NEG_INF;  // x-threshold cache
 
   // One exchange of per-wave insert counts and running maxima over one barrier; the
   // buffer is compacted when the round could overflow it.  Returns this wave's first
@@ -1067,8 +1120,8 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
         return U;
       },
       [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
-        float z[PF][G];
-        float lm = NEG_INF;
+        float xm[PF][G];
+        float lx = NEG_INF;
 #pragma unroll
         for (int k = 0; k < PF; ++k) {
           const int t = t0 + k;
@@ -1076,14 +1129,14 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
             const int base = t * TILE + tid * G;
             float x[G];
             unpack(R[k], x);
-            if ((t + 1) * TILE <= p.V) make_z<G, false>(x, base, p, h.bitmap, z[k], bad);
-            else make_z<G, true>(x, base, p, h.bitmap, z[k], bad);
+            if ((t + 1) * TILE <= p.V) mask_x<G, false>(x, base, p, h.bitmap, xm[k], nfx, ax);
+            else mask_x<G, true>(x, base, p, h.bitmap, xm[k], nfx, ax);
           } else {
 #pragma unroll
-            for (int j = 0; j < G; ++j) z[k][j] = NEG_INF;
+            for (int j = 0; j < G; ++j) xm[k][j] = NEG_INF;
           }
 #pragma unroll
-          for (int j = 0; j < G; ++j) lm = fmaxf(lm, z[k][j]);
+          for (int j = 0; j < G; ++j) lx = fmaxf(lx, xm[k][j]);
         }
         // the batch's first NT history slots, penalized exactly
         float zg = NEG_INF;
@@ -1094,10 +1147,16 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
           zg = pen_z(gx, count_of(h, s), p);
           if (!isfinite(zg)) bad = 1;
         }
-        lm = fmaxf(lm, zg);
-        wm = fmaxf(wm, wave_max_dpp(lm));
+        // RN(x/T) is non-decreasing in x, so the largest z is the quotient of the largest x
+        const float lz = lx > NEG_INF ? lx / p.T : NEG_INF;
+        wm = fmaxf(wm, wave_max_dpp(fmaxf(lz, zg)));
         const float bnd = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
-        const float th = tau;
+        if (!(tau == c_tau && bnd == c_bnd)) {
+          c_tau = tau;
+          c_bnd = bnd;
+          c_thr = x_threshold(tau, bnd, p);
+        }
+        const float th = c_thr;
         const uint64_t tk = tau_key;
         // stream elements: later tiles hold larger indices, so z > tau suffices against
         // the k-th key; history tokens arrive out of order and compare full keys
@@ -1107,7 +1166,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
         for (int k = 0; k < PF; ++k)
 #pragma unroll
           for (int j = 0; j < G; ++j) {
-            bal[k * G + j] = __ballot(z[k][j] > th && z[k][j] >= bnd);
+            bal[k * G + j] = __ballot(xm[k][j] >= th);
             wn += (uint32_t)__popcll(bal[k * G + j]);
           }
         const uint64_t kg = ckey(zg, tg);
@@ -1122,8 +1181,9 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
               if ((bal[e] >> lane) & 1ull) {
                 const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[e] >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal[e], 0u));
-                const uint64_t key = e == NE - 1 ? kg
-                                                 : ckey(z[e / G][e % G], (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
+                const uint64_t key =
+                    e == NE - 1 ? kg
+                                : ckey(xm[e / G][e % G] / p.T, (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
                 cand[pos + below] = key;
               }
               pos += (int)__popcll(bal[e]);
@@ -1134,11 +1194,11 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
           // the batch does not fit: one round per tile, then the history round
 #pragma unroll
           for (int k = 0; k < PF; ++k) {
-            const float th2 = tau;
+            const float th2 = x_threshold(tau, bnd, p);
             const int base = (t0 + k) * TILE + tid * G;
             round([&](int j, uint64_t& key) {
-                    key = ckey(z[k][j], (uint32_t)(base + j));
-                    return z[k][j] > th2 && z[k][j] >= bnd;
+                    key = ckey(xm[k][j] / p.T, (uint32_t)(base + j));
+                    return xm[k][j] >= th2;
                   }, G);
           }
           const uint64_t tk2 = tau_key;
@@ -1167,6 +1227,20 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
                 }, 1);
         }
       });
+  // raw non-finite logits make z non-finite (penalties keep infinities and NaN)
+  if (nfx) bad = 1;
+  // a finite x can still overflow x / T; rare, so such rows re-check every element
+  const float axw = wave_max_dpp(ax);
+  if (!isfinite(axw / p.T)) atomicOr(&m->status, 16);
+  __syncthreads();
+  if (m->status & 16) {
+    for (int i = tid; i < p.V; i += NT) {
+      const bool pen = p.has_pen && ((h.bitmap[i >> 5] >> (i & 31)) & 1u);
+      if (!pen && !isfinite(load_one<TIn>(rs, i) / p.T)) bad = 1;
+    }
+    __syncthreads();
+    if (tid == 0) m->status &= ~16;
+  }
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
 
