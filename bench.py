@@ -203,18 +203,93 @@ def main():
         copy_calibration(args.copy_bytes, args.steps, torch)
         return
     line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
+    print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
-        try:
-            from dsv41_rocm import logprob as _lp  # noqa: F401
-        except ImportError:
-            _lp = None
-        if _lp is not None:
-            line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, torch)
+        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, not args.no_cpu_baseline, torch)
     print(json.dumps(line), flush=True)
 
 
-def bench_logprob(name, steps, warmup, torch):
-    raise NotImplementedError
+def bench_logprob(name, steps, warmup, cpu_baseline, torch):
+    """Fused selected-token log-prob over one batch of config C or D (D adds the ratio)."""
+    from dsv41_rocm import _lib, selected_log_probs, workloads
+
+    cfg = workloads.LOGPROB_CONFIGS[name]
+    dev = torch.device("cuda:0")
+    print(f"[bench] generating log-prob config {name} on the GPU", file=sys.stderr, flush=True)
+    inp = workloads.logprob_inputs(name, device=dev)
+    x, w, t = inp["x"], inp["w"], inp["targets"]
+    n, h = x.shape
+    v = w.shape[0]
+    behavior = None
+    if cfg.ratio:
+        lp0 = selected_log_probs(x, w, t, 1.0)[0]
+        behavior = (lp0 + 0.05 * torch.randn(n, generator=inp["generator"], device=dev)).contiguous()
+    lp = torch.empty(n, dtype=torch.float32, device=dev)
+    ent = torch.empty(n, dtype=torch.float32, device=dev)
+    ratio = torch.empty(n, dtype=torch.float32, device=dev)
+    status = torch.empty(n, dtype=torch.int32, device=dev)
+    d = _lib.LogprobDesc()
+    d.struct_size = ctypes.sizeof(_lib.LogprobDesc)
+    d.n_tokens, d.hidden, d.vocab = n, h, v
+    d.x, d.x_row_stride, d.w, d.w_row_stride = x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0)
+    d.targets = t.data_ptr()
+    d.temperature = 1.0
+    if behavior is not None:
+        d.behavior, d.is_cap, d.out_ratio = behavior.data_ptr(), 2.0, ratio.data_ptr()
+    d.out_logprob, d.out_entropy, d.out_status = lp.data_ptr(), ent.data_ptr(), status.data_ptr()
+    lib = _lib.load()
+    ws_bytes = lib.dsv41_logprob_workspace_bytes(ctypes.byref(d))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        _lib.check(lib.dsv41_logprob_run(ctypes.byref(d), ws.data_ptr(), ws_bytes, stream))
+
+    ms = events_time(step, steps, warmup, torch)
+    assert int(status.max().item()) == 0, "log-prob reported a bad token"
+    flops = 2.0 * n * h * v
+    achieved = flops / (ms * 1e-3) / 1e12
+    out = {
+        "metric": "fused selected-token log-prob tok/s",
+        "value": n / (ms * 1e-3),
+        "unit": "tok/s",
+        "ms_per_step": ms,
+        "steps": steps,
+        "dtype": "bf16",
+        "config": {"workload": f"{name}: {n} tokens x hidden {h} -> vocab {v}"
+                               + (", Token-TIS ratio" if cfg.ratio else ""),
+                   "tokens": n, "hidden": h, "vocab": v},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": MEASURED_TRAFFIC.get(f"logprob_{name}"),
+                     "flops_per_token": 2.0 * h * v},
+    }
+    if cpu_baseline:
+        out["cpu_baseline"] = cpu_logprob_baseline(x, w, t, torch)
+    return out
+
+
+def cpu_logprob_baseline(x, w, t, torch):
+    """The reference expression log_softmax(linear(x, w).float() / T).gather(targets)
+    (model.py:682-683, native_lora.py:81-82) on the host, bf16 linear, on a token subset."""
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    wc = w.cpu()
+    xc, tc = x.cpu(), t.cpu()
+
+    def run(k):
+        logits = torch.nn.functional.linear(xc[:k], wc).float() / 1.0
+        return torch.log_softmax(logits, dim=-1).gather(-1, tc[:k, None]).squeeze(-1)
+
+    t0 = time.perf_counter()
+    run(16)
+    per_tok = (time.perf_counter() - t0) / 16
+    k = int(max(16, min(512, 15.0 / max(per_tok, 1e-6))))
+    t0 = time.perf_counter()
+    run(k)
+    dt = time.perf_counter() - t0
+    return {"value": k / dt, "unit": "tok/s", "cores": cores, "kind": "reference",
+            "sample": f"reference expression (bf16 linear, fp32 log_softmax, gather) on the first {k} "
+                      f"tokens, {dt:.1f} s on {cores} host cores"}
 
 
 if __name__ == "__main__":

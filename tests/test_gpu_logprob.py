@@ -1,0 +1,120 @@
+"""GPU parity of the fused selected-token log-prob (libdsv41hip.so through the C ABI).
+
+Reference values: fp64 log-softmax of fp64 logits computed from the same bf16 operands
+on the GPU (exact products, fp64 accumulation), plus the numpy fp64 oracle on a subset.
+Bar: log-prob, entropy and Token-TIS ratio within 1e-4 absolute.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dsv41_rocm import score_targets, selected_log_probs, token_log_probs, workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL = 1e-4
+
+
+def reference(x, w, t, temperature):
+    """fp64 log-prob and entropy from bf16 operands (on the GPU, chunked over tokens)."""
+    wd = w.double()
+    lps, ents = [], []
+    for s in range(0, x.shape[0], 256):
+        z = (x[s:s + 256].double() @ wd.T) / temperature
+        lsm = torch.log_softmax(z, dim=-1)
+        lps.append(lsm.gather(1, t[s:s + 256, None])[:, 0])
+        ents.append(-(lsm.exp() * lsm).sum(dim=1))
+    return torch.cat(lps), torch.cat(ents)
+
+
+def check(x, w, t, temperature, behavior=None, cap=2.0):
+    print(f"case: N={x.shape[0]} H={x.shape[1]} V={w.shape[0]} T={temperature} ratio={behavior is not None}",
+          flush=True)
+    lp, ent, ratio = selected_log_probs(x, w, t, temperature, behavior=behavior, is_cap=cap)
+    torch.cuda.synchronize()
+    rlp, rent = reference(x, w, t, temperature)
+    assert torch.max(torch.abs(lp.double() - rlp)).item() <= TOL
+    assert torch.max(torch.abs(ent.double() - rent)).item() <= TOL
+    if behavior is not None:
+        w_ref, _ = oracle.token_tis_weight(rlp.float().cpu().numpy(), behavior.cpu().numpy(), cap)
+        assert np.max(np.abs(ratio.cpu().numpy() - w_ref)) <= TOL
+    return lp, ent, ratio
+
+
+def test_config_c_shape_reduced_tokens():
+    inp = workloads.logprob_inputs("C", tokens=512, device=DEV)
+    check(inp["x"], inp["w"], inp["targets"], 1.0)
+
+
+def test_config_d_shape_reduced_tokens_with_ratio():
+    inp = workloads.logprob_inputs("D", tokens=384, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    rlp, _ = reference(inp["x"], inp["w"], inp["targets"], 1.0)
+    behavior = (rlp + 0.05 * torch.randn(rlp.shape, generator=g, device=DEV, dtype=torch.float64)).float()
+    check(inp["x"], inp["w"], inp["targets"], 1.0, behavior=behavior)
+
+
+def test_numpy_oracle_subset_agrees():
+    inp = workloads.logprob_inputs("C", tokens=256, device=DEV)
+    lp, ent, _ = selected_log_probs(inp["x"], inp["w"], inp["targets"], 0.8)
+    idx = torch.arange(0, 256, 37)
+    olp, oent = oracle.logprob_oracle(inp["x"][idx].float().cpu().numpy(), inp["w"].float().cpu().numpy(),
+                                      inp["targets"][idx].cpu().numpy(), 0.8)
+    assert np.max(np.abs(lp[idx].cpu().numpy() - olp)) <= TOL
+    assert np.max(np.abs(ent[idx].cpu().numpy() - oent)) <= TOL
+
+
+@pytest.mark.parametrize("n,h,v", [(1, 8, 1), (5, 40, 3), (130, 72, 257), (257, 136, 1000), (300, 2048, 4099),
+                                   (64, 64, 65536 + 17)])
+def test_ragged_shapes(n, h, v):
+    g = torch.Generator(device=DEV).manual_seed(n * 1000 + v)
+    x = torch.randn(n, h, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.3 * torch.randn(v, h, generator=g, device=DEV)).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g, device=DEV)
+    check(x, w, t, 0.7)
+
+
+def test_strided_hidden_and_empty_and_errors():
+    g = torch.Generator(device=DEV).manual_seed(9)
+    big = torch.randn(70, 200, generator=g, device=DEV).to(torch.bfloat16)
+    x = big[:, :192]  # row stride 200 (multiple of 8), 16-byte aligned rows
+    w = (0.2 * torch.randn(999, 192, generator=g, device=DEV)).to(torch.bfloat16)
+    t = torch.randint(0, 999, (70,), generator=g, device=DEV)
+    check(x, w, t, 1.3)
+    lp, ent, _ = selected_log_probs(x[:0], w, t[:0], 1.0)
+    assert lp.shape == (0,) and ent.shape == (0,)
+    with pytest.raises(ValueError, match="outside the model vocabulary"):
+        selected_log_probs(x, w, torch.full_like(t, 999), 1.0)
+    with pytest.raises(ValueError, match="temperature"):
+        selected_log_probs(x, w, t, 0.0)
+
+
+def test_drop_ins_match_reference_expression():
+    g = torch.Generator(device=DEV).manual_seed(3)
+    B, T, H, V = 2, 7, 64, 515
+    hidden = torch.randn(B, T, H, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.2 * torch.randn(V, H, generator=g, device=DEV)).to(torch.bfloat16)
+    targets = torch.randint(0, V, (B, T), generator=g, device=DEV)
+    mask = torch.rand(B, T, generator=g, device=DEV) > 0.3
+    out = token_log_probs(hidden, w, targets, mask, 0.8)
+    # model.py:682-684 with fp32 logits (the kernel does not round logits to bf16)
+    logits = (hidden[mask].double() @ w.double().T) / 0.8
+    sel = torch.log_softmax(logits, -1).gather(-1, targets[mask].unsqueeze(-1)).squeeze(-1)
+    expect = torch.zeros(B, T, dtype=torch.float64, device=DEV).masked_scatter(mask, sel)
+    assert out.dtype == torch.float32 and out.shape == (B, T)
+    assert torch.max(torch.abs(out.double() - expect)).item() <= TOL
+    assert torch.equal(out[~mask], torch.zeros_like(out[~mask]))
+    s = score_targets(hidden[mask], w, targets[mask], 0.8)
+    assert torch.equal(s, out[mask])
+    empty = token_log_probs(hidden, w, targets, torch.zeros_like(mask), 0.8)
+    assert torch.equal(empty, torch.zeros(B, T, device=DEV))
+
+
+def test_repeatable_bitwise():
+    inp = workloads.logprob_inputs("C", tokens=300, device=DEV)
+    a = selected_log_probs(inp["x"], inp["w"], inp["targets"], 1.0)
+    b = selected_log_probs(inp["x"], inp["w"], inp["targets"], 1.0)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
