@@ -1,0 +1,141 @@
+"""The C-ABI boundary without a GPU: libdsv41hip.so loads, exports every function that
+include/dsv41_rocm.h declares, its descriptor layouts agree with the ctypes mirrors field by
+field (offsets from gcc on the header), and invalid descriptors are rejected before any
+launch with the reference's messages."""
+
+import ctypes
+import json
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+from dsv41_rocm import _lib, sample, selected_log_probs
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dsv41_rocm.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(dsv41_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = declared_functions()
+    assert set(names) == set(_lib.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.dsv41_abi_version() == _lib.ABI_VERSION
+
+
+def test_descriptor_layouts_match_header(tmp_path):
+    fields = {"dsv41_sampler_desc": _lib.SamplerDesc, "dsv41_logprob_desc": _lib.LogprobDesc}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {", 'printf("{");']
+    first = True
+    for cname, cls in fields.items():
+        for fname, _ in cls._fields_:
+            sep = "" if first else ","
+            lines.append(f'printf("{sep}\\"{cname}.{fname}\\": %zu", offsetof({cname}, {fname}));')
+            first = False
+        lines.append(f'printf(",\\"{cname}.sizeof\\": %zu", sizeof({cname}));')
+    lines += ['printf("}\\n");', "return 0; }"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    got = json.loads(subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout)
+    for cname, cls in fields.items():
+        for fname, _ in cls._fields_:
+            assert getattr(cls, fname).offset == got[f"{cname}.{fname}"], (cname, fname)
+        assert ctypes.sizeof(cls) == got[f"{cname}.sizeof"]
+
+
+def _sampler_desc(**kw):
+    d = _lib.SamplerDesc()
+    d.struct_size = ctypes.sizeof(_lib.SamplerDesc)
+    d.rows, d.vocab, d.logits_dtype, d.logits_row_stride = 4, 100, _lib.DTYPE_F32, 100
+    d.logits, d.uniforms = 0x1000, 0x2000
+    d.out_ids, d.out_logprob, d.out_status = 0x3000, 0x4000, 0x5000
+    d.temperature, d.repetition_penalty, d.top_p = 1.0, 1.0, 1.0
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(temperature=0.0), _lib.E_INVALID, "temperature must be finite and positive"),
+    (dict(temperature=float("nan")), _lib.E_INVALID, "temperature must be finite and positive"),
+    (dict(top_p=0.0), _lib.E_INVALID, "top_p"),
+    (dict(top_k=-1), _lib.E_INVALID, "top_k"),
+    (dict(min_p=1.5), _lib.E_INVALID, "min_p"),
+    (dict(repetition_penalty=0.0), _lib.E_INVALID, "repetition_penalty"),
+    (dict(rows=0), _lib.E_INVALID, "shape"),
+    (dict(logits_row_stride=50), _lib.E_INVALID, "stride"),
+    (dict(uniforms=None), _lib.E_INVALID, "uniform"),
+    (dict(vocab=(1 << 21) + 1, logits_row_stride=(1 << 21) + 1), _lib.E_UNSUPPORTED, "2^21"),
+    (dict(struct_size=8), _lib.E_ABI, "size mismatch"),
+])
+def test_sampler_rejects_bad_descriptors_before_launch(kw, code, msg):
+    lib = _lib.load()
+    d = _sampler_desc(**kw)
+    assert lib.dsv41_sampler_run(ctypes.byref(d), None, 0, None) == code
+    assert msg in _lib.last_error()
+
+
+def test_sampler_workspace_only_for_the_radix_path():
+    lib = _lib.load()
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc())) == 0
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(top_k=5))) == 0
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(top_p=0.9))) == 4 * 100 * 4
+    d = _sampler_desc(top_p=0.9)
+    assert lib.dsv41_sampler_run(ctypes.byref(d), None, 0, None) == _lib.E_WORKSPACE
+
+
+def _logprob_desc(**kw):
+    d = _lib.LogprobDesc()
+    d.struct_size = ctypes.sizeof(_lib.LogprobDesc)
+    d.n_tokens, d.hidden, d.vocab = 10, 64, 300
+    d.x, d.x_row_stride, d.w, d.w_row_stride = 0x1000, 64, 0x2000, 64
+    d.targets, d.out_logprob, d.temperature = 0x3000, 0x4000, 1.0
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(temperature=-1.0), _lib.E_INVALID, "temperature must be finite and positive"),
+    (dict(hidden=60, x_row_stride=64, w_row_stride=64), _lib.E_UNSUPPORTED, "multiple of 8"),
+    (dict(x_row_stride=60), _lib.E_INVALID, "stride"),
+    (dict(x=0x1008), _lib.E_INVALID, "aligned"),
+    (dict(out_ratio=0x5000), _lib.E_INVALID, "behavior"),
+    (dict(behavior=0x6000, is_cap=0.0), _lib.E_INVALID, "is_cap"),
+])
+def test_logprob_rejects_bad_descriptors_before_launch(kw, code, msg):
+    lib = _lib.load()
+    d = _logprob_desc(**kw)
+    assert lib.dsv41_logprob_run(ctypes.byref(d), None, 0, None) == code
+    assert msg in _lib.last_error()
+
+
+def test_logprob_workspace_and_empty_batch():
+    lib = _lib.load()
+    d = _logprob_desc()
+    ws = lib.dsv41_logprob_workspace_bytes(ctypes.byref(d))
+    assert ws > 0 and ws % (16 * 10) == 0  # splits x tokens x 16-byte states
+    assert lib.dsv41_logprob_run(ctypes.byref(d), None, 0, None) == _lib.E_WORKSPACE
+    empty = _logprob_desc(n_tokens=0)
+    assert lib.dsv41_logprob_run(ctypes.byref(empty), None, 0, None) == _lib.OK
+
+
+def test_python_entry_points_fail_loudly_off_gpu():
+    with pytest.raises(ValueError, match="GPU"):
+        sample(torch.zeros(2, 10))
+    with pytest.raises(ValueError, match="temperature"):
+        sample(torch.zeros(2, 10), temperature=0.0)
+    with pytest.raises(ValueError, match="GPU"):
+        selected_log_probs(torch.zeros(3, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
+                           torch.zeros(3, dtype=torch.int64))

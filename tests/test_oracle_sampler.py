@@ -1,0 +1,226 @@
+"""Pins the C oracle of the sampler (oracle/sampler_oracle.c) without a GPU.
+
+Every check compares the oracle with something it does not share code with: libm's exp,
+Python's exact integers and fractions, torch's log_softmax in fp64, hand-derived penalty
+values, brute force over every prefix on tiny vocabularies, and the known answers of the
+reference's rollout tests (tests/golden/rollout_transition_model.json).
+"""
+
+import json
+import math
+import random
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLDEN = Path(__file__).parent / "golden"
+TWO43 = 1 << 43
+
+
+def test_exp_det_matches_libm_within_two_ulp():
+    rng = random.Random(1)
+    pts = [0.0, -1e-300, -0.5, -1.0, -math.log(2), -10.0, -29.9, -39.999] + [-40 * rng.random() for _ in range(20000)]
+    for d in pts:
+        e, ref = oracle.exp_det(d), math.exp(d)
+        assert abs(e - ref) <= 2 * math.ulp(ref), (d, e, ref)
+    assert oracle.exp_det(-40.0001) == 0.0 and oracle.exp_det(-1e9) == 0.0
+    assert oracle.exp_det(float("nan")) == 0.0
+    assert oracle.exp_det(0.25) == 1.0  # positive differences clamp to 0 (z never exceeds zmax)
+
+
+def test_mass_is_floor_of_2_43_times_exp():
+    rng = random.Random(2)
+    for _ in range(5000):
+        z, zmax = np.float32(rng.uniform(-30, 10)), np.float32(rng.uniform(10, 20))
+        q = oracle.mass(float(z), float(zmax))
+        e = math.exp(float(z) - float(zmax))
+        assert abs(q - math.floor(e * TWO43)) <= 1
+    assert oracle.mass(3.0, 3.0) == TWO43
+
+
+def test_top_p_threshold_is_exact_ceiling():
+    rng = random.Random(3)
+    for _ in range(20000):
+        p = float(np.float32(rng.choice([rng.random(), 0.95, 0.98, 0.5, 1e-6, 0.999999, 1.0])))
+        if p <= 0.0:
+            continue
+        s = rng.randrange(1, 1 << 62)
+        want = math.ceil(Fraction(p) * s)
+        assert oracle.top_p_threshold(p, s) == want, (p, s)
+
+
+def test_draw_target_is_exact():
+    rng = random.Random(4)
+    for _ in range(20000):
+        u = float(np.float32(rng.random()))
+        s = rng.randrange(1, 1 << 62)
+        uu = math.floor(Fraction(u) * (1 << 32))
+        assert oracle.draw_target(u, s) == (s * uu) >> 32
+    assert oracle.draw_target(0.0, 12345) == 0
+
+
+def test_penalties_hand_derived():
+    # vLLM apply_penalties: repetition (divide positive, multiply non-positive), then
+    # frequency * count, then presence, each rounded in fp32
+    assert oracle.penalize(2.0, 1, 2.0, 0.0, 0.0) == 1.0
+    assert oracle.penalize(-2.0, 1, 2.0, 0.0, 0.0) == -4.0
+    assert oracle.penalize(0.0, 1, 2.0, 0.0, 0.0) == 0.0
+    assert oracle.penalize(1.0, 3, 1.0, 0.0, 0.5) == -0.5
+    assert oracle.penalize(1.0, 3, 1.0, 0.25, 0.5) == -0.75
+    assert oracle.penalize(3.0, 2, 1.5, 0.5, 0.25) == 1.0  # 3/1.5 = 2; 2 - 0.5 - 0.5
+    x, c, rp, pres, freq = 1.2345678, 7, 1.1, 0.3, 0.07
+    f32 = np.float32
+    want = f32(f32(f32(x) / f32(rp)) - f32(f32(freq) * f32(c))) - f32(pres)
+    assert oracle.penalize(x, c, rp, pres, freq) == float(want)
+
+
+@pytest.mark.parametrize("T", [0.6, 0.7, 1.3, 0.1, 7.77])
+def test_three_operation_division_is_ieee_on_guarded_range(T):
+    # the kernel divides by T with q = x*r, e = fma(-q, T, x), z = fma(e, r, q) when
+    # 2^-100 <= |x| < 2^100; 256 windows of 65536 consecutive bit patterns spread over
+    # that range (both signs, both edges included) must match IEEE division
+    win = 65536
+    for lo, hi in ((0x0D800000, 0x71800000), (0x8D800000, 0xF1800000)):
+        starts = [lo + (hi - lo - win) * i // 255 for i in range(256)]
+        bad = sum(oracle.check_division(T, s, s + win)[0] for s in starts)
+        assert bad == 0
+
+
+def test_division_scheme_fails_below_the_guard():
+    # the guard exists because the residual underflows for tiny |x|
+    n, first = oracle.check_division(0.7, 0x00000001, 0x00800000)
+    assert n > 0 and first < 0x00800000
+
+
+def _row_reference_lp(x, T, tok):
+    z = torch.tensor(x, dtype=torch.float32) / T
+    return float(torch.log_softmax(z.double(), dim=-1)[tok])
+
+
+def test_full_vocab_logprob_is_log_softmax_of_scaled_logits():
+    rng = np.random.default_rng(5)
+    x = (3 * rng.standard_normal((16, 5000))).astype(np.float32)
+    u = rng.random(16).astype(np.float32)
+    ids, lps, kept, st = oracle.sample(x, uniforms=u, temperature=0.7)
+    assert (st == 0).all() and (kept == 5000).all()
+    for r in range(16):
+        assert abs(lps[r] - _row_reference_lp(x[r], np.float32(0.7), ids[r])) <= 1e-5
+
+
+def test_draw_is_inverse_cdf_in_vocabulary_order():
+    # brute force: with exact integer masses the drawn token is the first whose
+    # cumulative mass exceeds floor(u * 2^32) * S >> 32
+    rng = np.random.default_rng(6)
+    for _ in range(300):
+        V = int(rng.integers(1, 9))
+        x = rng.standard_normal((1, V)).astype(np.float32)
+        u = np.array([rng.random()], np.float32)
+        ids, _, _, _ = oracle.sample(x, uniforms=u, temperature=1.0)
+        zmax = float(x[0].max())
+        q = [math.floor(math.exp(float(v) - zmax) * TWO43) for v in x[0]]
+        t = (sum(q) * math.floor(Fraction(float(u[0])) * (1 << 32))) >> 32
+        cum, want = 0, None
+        for i, qi in enumerate(q):
+            cum += qi
+            if cum > t:
+                want = i
+                break
+        assert ids[0] == want
+
+
+def _brute_kept(z, k, p, min_p):
+    """Independent restatement with Python sorting and exact fractions."""
+    V = len(z)
+    zmax = max(z)
+    order = sorted(range(V), key=lambda i: (-float(z[i]), i))
+    if min_p > 0:
+        lm = math.log(float(np.float32(min_p)))
+        order = [i for i in order if float(z[i]) - zmax >= lm]
+    if 0 < k < len(order):
+        order = order[:k]
+    if p < 1:
+        q = [math.floor(math.exp(float(z[i]) - zmax) * TWO43) for i in order]
+        thr = math.ceil(Fraction(float(np.float32(p))) * sum(q))
+        cum = 0
+        for n, qi in enumerate(q):
+            cum += qi
+            if cum >= thr:
+                order = order[:n + 1]
+                break
+    return sorted(order)
+
+
+def test_kept_sets_match_brute_force_on_tiny_vocabularies():
+    rng = np.random.default_rng(7)
+    for trial in range(600):
+        V = int(rng.integers(1, 13))
+        # coarse values so that ties are common
+        x = (np.round(rng.standard_normal(V) * 2) / 2).astype(np.float32)
+        k = int(rng.integers(0, V + 2))
+        p = float(rng.choice([1.0, 0.9, 0.5, 0.3]))
+        mp = float(rng.choice([0.0, 0.0, 0.2, 0.6]))
+        T = float(rng.choice([1.0, 0.7]))
+        z = (x / np.float32(T)).astype(np.float32)
+        want = _brute_kept(z, k, p, mp)
+        # greedy reveals nothing about the kept set, so draw with u at each kept item
+        _, _, kept, st = oracle.sample(x[None], uniforms=np.array([0.5], np.float32), temperature=T, top_k=k,
+                                       top_p=p, min_p=mp)
+        assert st[0] == 0 and kept[0] == len(want), (trial, x, k, p, mp)
+        # every kept token is drawable and only kept tokens are drawn
+        seen = set()
+        for u in np.linspace(0, 1, 97, endpoint=False):
+            ids, _, _, _ = oracle.sample(x[None], uniforms=np.array([u], np.float32), temperature=T, top_k=k,
+                                         top_p=p, min_p=mp)
+            seen.add(int(ids[0]))
+        assert seen <= set(want)
+
+
+def test_identities_and_greedy_first_max():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((6, 300)).astype(np.float32)
+    x[:, 10] = x[:, 200] = x.max() + 1  # tie: greedy must pick index 10
+    u = rng.random(6).astype(np.float32)
+    base = oracle.sample(x, uniforms=u)
+    for knobs in (dict(top_k=300), dict(top_k=10 ** 6), dict(top_p=1.0), dict(min_p=0.0)):
+        got = oracle.sample(x, uniforms=u, **knobs)
+        assert np.array_equal(got[0], base[0]) and np.array_equal(got[2], base[2])
+    ids, _, _, _ = oracle.sample(x, greedy=True)
+    assert (ids == 10).all()
+    assert (ids == torch.argmax(torch.from_numpy(x), dim=1).numpy()).all()
+    ids, _, kept, _ = oracle.sample(x, uniforms=u, top_k=1)
+    assert (ids == 10).all() and (kept == 1).all()
+
+
+def test_status_rows():
+    x = np.zeros((4, 10), np.float32)
+    x[1, 3] = np.nan
+    x[2, 0] = -np.inf
+    h = np.zeros((4, 2), np.int64)
+    h[3, 0] = 99
+    u = np.array([0.5, 0.5, 0.5, 1.0], np.float32)
+    ids, lps, kept, st = oracle.sample(x, uniforms=u, history=h, repetition_penalty=1.2)
+    assert list(st) == [0, 1, 1, 2 | 4]
+    assert ids[1] == -1 and ids[2] == -1 and np.isnan(lps[1])
+
+
+def test_reference_rollout_toy_model_known_answers():
+    g = json.loads((GOLDEN / "rollout_transition_model.json").read_text())
+    T = g["temperature"]
+    rows = np.array(g["transitions"], np.float32)
+    for r in range(3):
+        for u in np.linspace(0, 1, 40, endpoint=False):
+            ids, lps, _, _ = oracle.sample(rows[r:r + 1], uniforms=np.array([u], np.float32), temperature=T)
+            # behaviour log-prob equals teacher forcing (test_rl_rollout.py:48-57)
+            assert abs(lps[0] - _row_reference_lp(rows[r], np.float32(T), ids[0])) <= 1e-6
+    eos = np.array([g["always_eos_row"]], np.float32)
+    ids, _, _, _ = oracle.sample(eos, uniforms=np.array([0.999], np.float32), temperature=T)
+    assert ids[0] == 2
+    zeros = np.zeros((1, 3), np.float32)
+    seen = {int(oracle.sample(zeros, uniforms=np.array([u], np.float32), temperature=T)[0][0])
+            for u in np.linspace(0, 1, 30, endpoint=False)}
+    assert seen == {0, 1, 2}  # every vocabulary token is reachable (test_rl_rollout.py:105-110)
