@@ -32,9 +32,13 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by
-# the same counters on a plain copy of known size (profiles/*_traffic.md).  None = not
-# measured for the current kernel build.
-MEASURED_TRAFFIC = {}
+# the same counters on a plain 1 GiB copy (FETCH x 2.0, WRITE x 1.0); the commands and raw
+# counts are in profiles/sampler_topk_E.md and profiles/logprob_fused_D.md.  Workloads
+# without an entry report null.
+MEASURED_TRAFFIC = {
+    "sampler_E": 2_649_526_272 + 575_480,
+    "logprob_D": 74_377_687_040 + 2_097_152,
+}
 
 
 def sampler_bytes_per_row(vocab, esize, hist_len):

@@ -139,3 +139,33 @@ def test_python_entry_points_fail_loudly_off_gpu():
     with pytest.raises(ValueError, match="GPU"):
         selected_log_probs(torch.zeros(3, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
                            torch.zeros(3, dtype=torch.int64))
+
+
+def test_custom_ops_registered_with_fake_kernels():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import dsv41_rocm  # noqa: F401
+
+    assert hasattr(torch.ops.dsv41_rocm, "sample_rows")
+    assert hasattr(torch.ops.dsv41_rocm, "selected_log_probs")
+    with FakeTensorMode():
+        x = torch.empty(4, 100, device="meta")
+        ids, lps, kept, st = torch.ops.dsv41_rocm.sample_rows(x, torch.empty(4, device="meta"), None, None,
+                                                              0.7, 1.0, 0.0, 0.0, 0, 1.0, 0.0, False)
+        assert ids.shape == (4,) and ids.dtype == torch.int64 and lps.dtype == torch.float32
+        assert kept.dtype == st.dtype == torch.int32
+        h = torch.empty(5, 16, dtype=torch.bfloat16, device="meta")
+        w = torch.empty(30, 16, dtype=torch.bfloat16, device="meta")
+        t = torch.empty(5, dtype=torch.int64, device="meta")
+        lp, ent, ratio = torch.ops.dsv41_rocm.selected_log_probs(h, w, t, 1.0, None, 2.0)
+        assert lp.shape == ent.shape == (5,) and ratio.shape == (0,)
+        lp, ent, ratio = torch.ops.dsv41_rocm.selected_log_probs(h, w, t, 1.0, torch.empty(5, device="meta"), 2.0)
+        assert ratio.shape == (5,)
+
+
+def test_custom_ops_have_no_cpu_kernel():
+    import dsv41_rocm  # noqa: F401
+
+    with pytest.raises(NotImplementedError):
+        torch.ops.dsv41_rocm.sample_rows(torch.zeros(2, 10), torch.rand(2), None, None,
+                                         1.0, 1.0, 0.0, 0.0, 0, 1.0, 0.0, False)

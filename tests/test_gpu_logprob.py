@@ -118,3 +118,15 @@ def test_repeatable_bitwise():
     a = selected_log_probs(inp["x"], inp["w"], inp["targets"], 1.0)
     b = selected_log_probs(inp["x"], inp["w"], inp["targets"], 1.0)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_custom_op_matches_wrapper():
+    inp = workloads.logprob_inputs("C", tokens=64, device=DEV)
+    x, w, t = inp["x"], inp["w"], inp["targets"]
+    print("case: torch.ops.dsv41_rocm.selected_log_probs on config C, 64 tokens", flush=True)
+    behavior = torch.full((64,), -12.0, device=DEV)
+    lp, ent, ratio = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, behavior, 2.0)
+    rlp, rent, rratio = selected_log_probs(x, w, t, 0.9, behavior=behavior, is_cap=2.0)
+    assert torch.equal(lp, rlp) and torch.equal(ent, rent) and torch.equal(ratio, rratio)
+    lp2, _, empty = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, None, 2.0)
+    assert torch.equal(lp2, rlp) and empty.numel() == 0

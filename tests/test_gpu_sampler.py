@@ -186,3 +186,16 @@ def test_repeatable_bitwise():
     a = sample(x, **args)
     b = sample(x, **args)
     assert torch.equal(a.ids, b.ids) and torch.equal(a.logprobs, b.logprobs) and torch.equal(a.kept, b.kept)
+
+
+def test_custom_op_matches_wrapper():
+    inp = workloads.sampler_inputs("A")
+    x, u, h = inp["logits"].to(DEV), inp["uniforms"].to(DEV), inp["history"].to(DEV)
+    k = inp["knobs"]
+    print("case: torch.ops.dsv41_rocm.sample_rows on config A", flush=True)
+    ids, lps, kept, st = torch.ops.dsv41_rocm.sample_rows(
+        x, u, h, None, k["temperature"], k.get("repetition_penalty", 1.0), k.get("presence_penalty", 0.0),
+        k.get("frequency_penalty", 0.0), k.get("top_k", 0), k.get("top_p", 1.0), k.get("min_p", 0.0), False)
+    ref = sample(x, uniforms=u, history=h, **k)
+    assert torch.equal(ids, ref.ids) and torch.equal(lps, ref.logprobs)
+    assert torch.equal(kept, ref.kept) and torch.equal(st, ref.status)

@@ -1,0 +1,85 @@
+"""torch.library custom ops over libdsv41hip.so, in the reference's operator idiom
+(``torch.library.custom_op(..., mutates_args=(), device_types="cuda")`` plus
+``register_fake``, dsv41_train/models/dsv4/moe/kernels.py:236-281).
+
+* ``dsv41_rocm::sample_rows`` — the row sampler; returns ``(ids, logprobs, kept, status)``.
+* ``dsv41_rocm::selected_log_probs`` — the fused log-prob head; returns
+  ``(logprob, entropy, ratio)`` with an empty ``ratio`` when no behaviour log-probs are given.
+
+The ops only register a CUDA (HIP) kernel: called on CPU tensors they raise, as the library
+has no CPU path.  Status bits are returned, not raised, so the ops stay traceable; the
+Python wrappers in ``sampling`` and ``logprob`` raise the reference's errors.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import logprob as _logprob
+from . import sampling as _sampling
+
+
+@torch.library.custom_op("dsv41_rocm::sample_rows", mutates_args=(), device_types="cuda")
+def sample_rows(
+    logits: torch.Tensor,
+    uniforms: Optional[torch.Tensor],
+    history: Optional[torch.Tensor],
+    history_lens: Optional[torch.Tensor],
+    temperature: float,
+    repetition_penalty: float,
+    presence_penalty: float,
+    frequency_penalty: float,
+    top_k: int,
+    top_p: float,
+    min_p: float,
+    greedy: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    if not greedy and uniforms is None:
+        raise ValueError("sampling requires one uniform per row")
+    r = _sampling.sample(logits, temperature=temperature, uniforms=uniforms, history=history,
+                         history_lens=history_lens, repetition_penalty=repetition_penalty,
+                         presence_penalty=presence_penalty, frequency_penalty=frequency_penalty,
+                         top_k=top_k, top_p=top_p, min_p=min_p, greedy=greedy, check=False)
+    return r.ids, r.logprobs, r.kept, r.status
+
+
+@sample_rows.register_fake
+def _sample_rows_fake(logits, uniforms, history, history_lens, temperature, repetition_penalty,
+                      presence_penalty, frequency_penalty, top_k, top_p, min_p, greedy):
+    rows = logits.shape[0]
+    dev = logits.device
+    return (torch.empty(rows, dtype=torch.int64, device=dev),
+            torch.empty(rows, dtype=torch.float32, device=dev),
+            torch.empty(rows, dtype=torch.int32, device=dev),
+            torch.empty(rows, dtype=torch.int32, device=dev))
+
+
+@torch.library.custom_op("dsv41_rocm::selected_log_probs", mutates_args=(), device_types="cuda")
+def selected_log_probs_op(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    targets: torch.Tensor,
+    temperature: float,
+    behavior: Optional[torch.Tensor],
+    is_cap: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    lp, ent, ratio = _logprob.selected_log_probs(hidden, weight, targets, temperature,
+                                                 behavior=behavior, is_cap=is_cap, check=False)
+    if ratio is None:
+        ratio = lp.new_empty(0)
+    return lp, ent, ratio
+
+
+@selected_log_probs_op.register_fake
+def _selected_log_probs_fake(hidden, weight, targets, temperature, behavior, is_cap):
+    n = hidden.shape[0]
+    dev = hidden.device
+    lp = torch.empty(n, dtype=torch.float32, device=dev)
+    ent = torch.empty(n, dtype=torch.float32, device=dev)
+    ratio = torch.empty(n if behavior is not None else 0, dtype=torch.float32, device=dev)
+    return lp, ent, ratio
+
+
+__all__ = ["sample_rows", "selected_log_probs_op"]
