@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="E", choices=["A", "B", "E"])
+    ap.add_argument("--workload", default="E", choices=["A", "B", "E", "none"],
+                    help="sampler config; 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
     ap.add_argument("--logprob-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -206,8 +207,11 @@ def main():
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.steps, torch)
         return
-    line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
-    print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
+    if args.workload == "none":
+        line = {}
+    else:
+        line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
+        print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
         line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, not args.no_cpu_baseline, torch)
     print(json.dumps(line), flush=True)

@@ -10,15 +10,20 @@
 // The contraction is computed transposed, C^T[v, n] = sum_k w[v, k] x[n, k], so that an
 // MFMA lane owns one token column and the per-token softmax state lives in registers:
 // each lane of a 32x32 output block holds 16 vocabulary rows of one token.  A workgroup
-// owns BT tokens and sweeps a slice of the vocabulary in BV-row blocks; after each
-// block its fp32 accumulators update a running (max, sum e, sum e*z, z_target) per
-// token, and slices are merged by a second kernel.
+// owns BT = 256 tokens and sweeps a range of the vocabulary in BV = 256-row blocks (each
+// of its four waves computes a 128 x 128 quarter); after each block the fp32
+// accumulators update a running (max, sum e, sum e*z, z_target) per token, and the
+// vocabulary ranges are merged by a second kernel.
 //
 // Operands move from HBM to LDS with buffer loads that write LDS directly (no register
-// staging), into two stage buffers so the next stage loads while this one multiplies.
-// Each 128-byte LDS row holds 64 bf16 of one matrix row with its 16-byte chunks
-// XOR-swizzled by (row & 7), so the MFMA fragment reads of 8 consecutive rows hit 8
-// different bank groups.
+// staging) into a ring of NBUF stage buffers, each holding 32 hidden elements of every
+// row, so loads run NBUF - 2 stages ahead of the multiplies.  The stage sequence runs
+// straight across vocabulary blocks, so the pipeline never drains between blocks.  MFMA
+// operand fragments are double-buffered in registers: the fragments of the next k-step
+// (including the first k-step of the next stage) are read from LDS while the current
+// k-step multiplies.  Each 64-byte LDS row holds 32 bf16 of one matrix row with its four
+// 16-byte chunks XOR-swizzled by ((row >> 1) ^ (row >> 3)) & 3, which puts any 16
+// consecutive rows of one chunk on distinct bank groups.
 
 #include <math.h>
 
@@ -27,14 +32,25 @@
 namespace dsv41 {
 namespace logprob {
 
-constexpr int NT = 256;     // 4 waves, 2 (vocab) x 2 (tokens)
-constexpr int WV = 4;       // 32-row MFMA blocks per wave along the vocabulary
-constexpr int WT = 2;       // 32-column MFMA blocks per wave along tokens
-constexpr int BV = 2 * WV * 32;  // 256 vocabulary rows per block
-constexpr int BT = 2 * WT * 32;  // tokens per workgroup
-constexpr int BK = 64;      // hidden elements per stage (128 bytes per row)
-constexpr int STAGE_BYTES = (BV + BT) * 128;
-constexpr int LDS_BYTES = 2 * STAGE_BYTES;  // two stage buffers
+constexpr int WAVES_V = 2;                   // waves along the vocabulary
+constexpr int WAVES_T = 4;                   // waves along tokens
+constexpr int NWAVES = WAVES_V * WAVES_T;
+constexpr int NT = 64 * NWAVES;              // 8 waves, two per SIMD
+constexpr int WV = 4;                        // 32-row MFMA blocks per wave along the vocabulary
+constexpr int WT = 2;                        // 32-column MFMA blocks per wave along tokens
+constexpr int BV = WAVES_V * WV * 32;        // 256 vocabulary rows per block
+constexpr int BT = WAVES_T * WT * 32;        // 256 tokens per workgroup
+constexpr int BK = 32;                       // hidden elements per stage
+constexpr int KS = BK / 16;                  // MFMA k-steps per stage
+constexpr int ROWB = BK * 2;                 // bytes per LDS row
+constexpr int STAGE_BYTES = (BV + BT) * ROWB;  // 32 KiB
+constexpr int NBUF = 5;                      // stage ring depth
+constexpr int LDS_BYTES = NBUF * STAGE_BYTES;  // 160 KiB
+constexpr int ROWS_PER_LOAD = 1024 / ROWB;   // rows one wave-wide 16-byte LDS load fills
+constexpr int A_LOADS = BV / NWAVES / ROWS_PER_LOAD;  // per wave per stage
+constexpr int B_LOADS = BT / NWAVES / ROWS_PER_LOAD;
+constexpr int LOADS = A_LOADS + B_LOADS;     // vmcnt units one stage adds per wave
+constexpr int CU_COUNT = 256;                // MI355X
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -49,10 +65,10 @@ struct Params {
   const uint16_t* w;
   int64_t ws;
   const int64_t* targets;
-  float4* part;  // [splits][N] (max, sum e, sum e*z, z_target or NaN)
+  float4* part;  // [splits][N] (max z, sum e, sum e*z, unused)
   int N, H, V;
   float invT;
-  int splits, vb_per_split, n_vb, n_tb;
+  int splits, n_vb, n_tb;
   int group_t, group_s;  // XCD super-tile shape (0: linear mapping)
 };
 
@@ -90,153 +106,214 @@ __device__ __forceinline__ void block_coords(const Params& p, int b, int& tb, in
   }
 }
 
-__global__ __launch_bounds__(NT, 1) void fused_kernel(Params p) {
+// Bank-group swizzle of the 16-byte chunks of LDS row `row`.  It depends only on
+// row % 16, so rows 32 apart (MFMA blocks) and rows 64 apart (waves' load ranges) share it.
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+// Waits until at most `newer` stages of this wave's LDS loads are outstanding.
+__device__ __forceinline__ void wait_loads(int newer) {
+  static_assert(2 * LOADS <= 63, "vmcnt encodings below");
+  // s_waitcnt vmcnt(n), expcnt/lgkmcnt at their maxima: n[3:0] in bits 3:0, n[5:4] in bits 15:14
+  if (newer >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * LOADS) & 15) | (((2 * LOADS) >> 4) << 14));
+  else if (newer == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS & 15) | ((LOADS >> 4) << 14));
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// Workgroup barrier with no memory fence: completion of the LDS loads is tracked with
+// vmcnt above, and the memory clobber keeps the compiler from moving LDS accesses across.
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ void read_frags(const unsigned char* stage, int addr_a, int addr_b, bf16x8 (&fa)[WV],
+                                           bf16x8 (&fb)[WT]) {
+#pragma unroll
+  for (int i = 0; i < WV; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(stage + addr_a + i * 32 * ROWB);
+#pragma unroll
+  for (int j = 0; j < WT; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(stage + addr_b + j * 32 * ROWB);
+}
+
+// Folds one vocabulary block into the running (max z, sum e, sum e*z) of token column j.
+// Rows at offsets >= lim lie past the vocabulary (their weights read as zero) and are
+// skipped when MASK is set.
+template <bool MASK>
+__device__ __forceinline__ void absorb(const floatx16 (&acc)[WV][WT], int j, int lim, float invT, float& m,
+                                       float& s, float& a) {
+  float mx = NEG_INF;
+#pragma unroll
+  for (int i = 0; i < WV; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int off = i * 32 + 8 * (r >> 2) + (r & 3);
+      mx = fmaxf(mx, (!MASK || off < lim) ? acc[i][j][r] : NEG_INF);
+    }
+  const float mn = fmaxf(m, mx * invT);  // invT > 0: the max commutes with the scaling
+  if (mn == NEG_INF) return;
+  const float c1 = invT * LOG2E, mb = mn * LOG2E;
+  float sum = 0.0f, ea = 0.0f;
+#pragma unroll
+  for (int i = 0; i < WV; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int off = i * 32 + 8 * (r >> 2) + (r & 3);
+      const float v = acc[i][j][r];
+      const float e = exp2f((!MASK || off < lim) ? __builtin_fmaf(v, c1, -mb) : NEG_INF);
+      sum += e;
+      ea = __builtin_fmaf(e, v, ea);
+    }
+  const float cs = exp2f((m - mn) * LOG2E);
+  s = __builtin_fmaf(s, cs, sum);
+  a = __builtin_fmaf(a, cs, ea * invT);
+  m = mn;
+}
+
+__global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void fused_kernel(Params p) {
   __shared__ __align__(16) unsigned char lds[LDS_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wv = wid & 1, wt = wid >> 1;
+  const int wv = wid % WAVES_V, wt = wid / WAVES_V;
   int tb, split;
   block_coords(p, blockIdx.x, tb, split);
   const int t0 = tb * BT;
-  const int vb0 = split * p.vb_per_split;
-  const int vb1 = min(vb0 + p.vb_per_split, p.n_vb);
+  const int vb0 = (int)((int64_t)split * p.n_vb / p.splits);
+  const int vb1 = (int)((int64_t)(split + 1) * p.n_vb / p.splits);
+  const int nst = (p.H + BK - 1) / BK;  // stages per vocabulary block
+  const int total = (vb1 - vb0) * nst;  // stages of this workgroup
 
-  // token columns of this lane and their targets
-  int tgt[WT];
-  float m_[WT], s_[WT], a_[WT], zt_[WT];
+  float m_[WT], s_[WT], a_[WT];
 #pragma unroll
   for (int j = 0; j < WT; ++j) {
-    const int n = t0 + wt * (WT * 32) + j * 32 + (lane & 31);
-    tgt[j] = n < p.N ? (int)p.targets[n] : -1;
     m_[j] = NEG_INF;
     s_[j] = 0.0f;
     a_[j] = 0.0f;
-    zt_[j] = __builtin_nanf("");
   }
 
+  // Loader.  Wave w fills rows [R*w, R*w + R) of the weight block and of the token block,
+  // R = 256 / NWAVES; lane l of load q fills slot l%4 of row R*w + 16q + l/4 with global
+  // chunk (l%4) ^ swz(row) = (l%4) ^ swz(l/4) ^ (2q & 3).  Chunks at or past the hidden
+  // size (only in a final partial stage) get bit 31 of the offset set, past every buffer,
+  // so they read zero.
+  constexpr int R = BV / NWAVES;
+  static_assert(BV == BT && R % 16 == 0 && ROWS_PER_LOAD == 16, "loader layout");
   const int rows_x = min(BT, p.N - t0);
   const __amdgpu_buffer_rsrc_t rx = rsrc(p.x + (int64_t)t0 * p.xs, (uint32_t)(rows_x * p.xs * 2));
-  const int nst = (p.H + BK - 1) / BK;
-
-  // Wave w loads rows [w*BV/4, (w+1)*BV/4) of the weight block and rows
-  // [w*BT/4, (w+1)*BT/4) of the token block, 8 rows of 128 bytes per instruction.
-  // Lane l fills slot l%8 of row l/8, which holds global chunk (l%8) ^ (row & 7).
-  constexpr int A_ROWS = BV / 4, B_ROWS = BT / 4;
-  static_assert(A_ROWS % 8 == 0 && B_ROWS % 8 == 0, "whole instructions per wave");
-  const int lrow = lane >> 3, lslot = lane & 7;
-  auto issue_stage = [&](__amdgpu_buffer_rsrc_t rw, int st, int buf) {
-    const int k0 = st * BK;
-    unsigned char* base = lds + buf * STAGE_BYTES;
-#pragma unroll
-    for (int q = 0; q < A_ROWS / 8; ++q) {
-      const int row = wid * A_ROWS + q * 8 + lrow;
-      const int kc = k0 + ((lslot ^ (row & 7)) << 3);
-      // chunks past the hidden size get bit 31 set: beyond every row, so they read zero
-      const uint32_t off = (uint32_t)((row * p.ws + kc) * 2) | ((uint32_t)(kc >= p.H) << 31);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (wid * A_ROWS + q * 8) * 128), 16, off, 0,
-                                               0, 0);
+  const int lrow = wid * R + (lane >> 2);
+  const int lch = (lane & 3) ^ swz(lane >> 2);  // global chunk for even q; odd q use lch ^ 2
+  const uint32_t la = (uint32_t)(lrow * p.ws * 2), lb = (uint32_t)(lrow * p.xs * 2);
+  const uint32_t qa = (uint32_t)(16 * p.ws * 2), qb = (uint32_t)(16 * p.xs * 2);
+  int ld = 0, ld_k = 0, ld_vb = vb0, lbuf = 0;
+  auto w_rsrc = [&](int vb) {
+    const int v0 = vb * BV;
+    return rsrc(p.w + (int64_t)v0 * p.ws, (uint32_t)(min(BV, p.V - v0) * p.ws * 2));
+  };
+  __amdgpu_buffer_rsrc_t rw_ld = w_rsrc(vb0);
+  auto issue_next = [&]() {
+    unsigned char* base = lds + lbuf * STAGE_BYTES;
+    const int k0 = ld_k * BK;
+    uint32_t c0 = (uint32_t)((k0 + 8 * lch) * 2), c1 = (uint32_t)((k0 + 8 * (lch ^ 2)) * 2);
+    if (k0 + BK > p.H) {
+      c0 |= (uint32_t)(k0 + 8 * lch >= p.H) << 31;
+      c1 |= (uint32_t)(k0 + 8 * (lch ^ 2) >= p.H) << 31;
     }
 #pragma unroll
-    for (int q = 0; q < B_ROWS / 8; ++q) {
-      const int row = wid * B_ROWS + q * 8 + lrow;
-      const int kc = k0 + ((lslot ^ (row & 7)) << 3);
-      const uint32_t off = (uint32_t)((row * p.xs + kc) * 2) | ((uint32_t)(kc >= p.H) << 31);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + BV * 128 + (wid * B_ROWS + q * 8) * 128), 16,
-                                               off, 0, 0, 0);
+    for (int q = 0; q < A_LOADS; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw_ld, (lds_ptr_t)(base + (wid * R + q * 16) * ROWB), 16,
+                                               la + q * qa + ((q & 1) ? c1 : c0), 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < B_LOADS; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + (BV + wid * R + q * 16) * ROWB), 16,
+                                               lb + q * qb + ((q & 1) ? c1 : c0), 0, 0, 0);
+    ++ld;
+    if (++lbuf == NBUF) lbuf = 0;
+    if (++ld_k == nst) {
+      ld_k = 0;
+      if (++ld_vb < vb1) rw_ld = w_rsrc(ld_vb);
     }
   };
 
-  for (int vb = vb0; vb < vb1; ++vb) {
-    const int v0 = vb * BV;
-    const int rows_w = min(BV, p.V - v0);
-    const __amdgpu_buffer_rsrc_t rw = rsrc(p.w + (int64_t)v0 * p.ws, (uint32_t)(rows_w * p.ws * 2));
-    floatx16 acc[WV][WT];
+  // Fragment reads: lane l takes row l%32 of each 32-row block and 8 values of chunk
+  // 2*ks + l/32, stored at slot chunk ^ swz(l%32).
+  const int r32 = lane & 31, half = lane >> 5;
+  const int fa_base = (wv * (WV * 32) + r32) * ROWB, fb_base = (BV + wt * (WT * 32) + r32) * ROWB;
+  int fch[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) fch[ks] = ((2 * ks + half) ^ swz(r32)) << 4;
+
+  floatx16 acc[WV][WT];
+#pragma unroll
+  for (int i = 0; i < WV; ++i)
+#pragma unroll
+    for (int j = 0; j < WT; ++j) acc[i][j] = floatx16{};
+
+  // prologue: NBUF - 1 stages in flight, stage 0 landed, its first fragments in registers
+#pragma unroll
+  for (int q = 0; q < NBUF - 1; ++q)
+    if (ld < total) issue_next();
+  wait_loads(min(total - 1, NBUF - 2));
+  barrier();
+  bf16x8 fa[WV], fb[WT];
+  read_frags(lds, fa_base + fch[0], fb_base + fch[0], fa, fb);
+
+  int vb = vb0, kst = 0, cbuf = 0;  // block, k-slice and buffer of the stage being multiplied
+  for (int st = 0; st < total; ++st) {
+    const unsigned char* stage = lds + cbuf * STAGE_BYTES;
+    const int nbuf = cbuf + 1 == NBUF ? 0 : cbuf + 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      bf16x8 na[WV], nb[WT];
+      if (ks + 1 < KS) {
+        read_frags(stage, fa_base + fch[ks + 1], fb_base + fch[ks + 1], na, nb);
+      } else if (st + 1 < total) {
+        // stage st+1 must have landed for every wave before its fragments are read, and
+        // every wave must be done with stage st-1 before its buffer is refilled
+        wait_loads(min(total - 1, st + NBUF - 2) - (st + 1));
+        barrier();
+        if (ld < total) issue_next();
+        read_frags(lds + nbuf * STAGE_BYTES, fa_base + fch[0], fb_base + fch[0], na, nb);
+      }
+#pragma unroll
+      for (int i = 0; i < WV; ++i)
+#pragma unroll
+        for (int j = 0; j < WT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < WV; ++i) fa[i] = na[i];
+#pragma unroll
+      for (int j = 0; j < WT; ++j) fb[j] = nb[j];
+    }
+    cbuf = nbuf;
+    if (++kst < nst) continue;
+
+    // end of a vocabulary block: lane holds rows 8*(r/4) + 4*(lane/32) + r%4 of each
+    // 32-row block, at offsets from rbase that are compile-time constants
+    const int rbase = vb * BV + wv * (WV * 32) + 4 * half;
+    if ((vb + 1) * BV <= p.V) {
+#pragma unroll
+      for (int j = 0; j < WT; ++j) absorb<false>(acc, j, 0, p.invT, m_[j], s_[j], a_[j]);
+    } else {
+      const int lim = p.V - rbase;
+#pragma unroll
+      for (int j = 0; j < WT; ++j) absorb<true>(acc, j, lim, p.invT, m_[j], s_[j], a_[j]);
+    }
 #pragma unroll
     for (int i = 0; i < WV; ++i)
 #pragma unroll
       for (int j = 0; j < WT; ++j) acc[i][j] = floatx16{};
-
-    __syncthreads();  // the previous block's last stage has been read
-    issue_stage(rw, 0, 0);
-    for (int st = 0; st < nst; ++st) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stage data is in LDS
-      __syncthreads();                     // all waves' data in; buffer st+1 is free
-      if (st + 1 < nst) issue_stage(rw, st + 1, (st + 1) & 1);
-      const unsigned char* A = lds + (st & 1) * STAGE_BYTES;
-      const unsigned char* B = A + BV * 128;
-#pragma unroll
-      for (int ks = 0; ks < BK / 16; ++ks) {
-        const int c = ks * 2 + (lane >> 5);  // chunk of this lane's 8 values
-        bf16x8 fa[WV], fb[WT];
-#pragma unroll
-        for (int i = 0; i < WV; ++i) {
-          const int row = wv * (WV * 32) + i * 32 + (lane & 31);
-          fa[i] = *reinterpret_cast<const bf16x8*>(A + row * 128 + ((c ^ (row & 7)) << 4));
-        }
-#pragma unroll
-        for (int j = 0; j < WT; ++j) {
-          const int row = wt * (WT * 32) + j * 32 + (lane & 31);
-          fb[j] = *reinterpret_cast<const bf16x8*>(B + row * 128 + ((c ^ (row & 7)) << 4));
-        }
-#pragma unroll
-        for (int i = 0; i < WV; ++i)
-#pragma unroll
-          for (int j = 0; j < WT; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-      }
-    }
-
-    // epilogue: lane holds rows 8*(r/4) + 4*(lane/32) + r%4 of each 32-row block; the
-    // running state absorbs one 16-value block at a time
-    // positions are compared relative to this lane's first row, so each (i, r) is a
-    // compile-time offset
-    const int rbase = v0 + wv * (WV * 32) + 4 * (lane >> 5);
-    const int lim = p.V - rbase;  // offsets below lim are rows of the vocabulary
-#pragma unroll
-    for (int j = 0; j < WT; ++j) {
-      const int dt = tgt[j] - rbase;
-#pragma unroll
-      for (int i = 0; i < WV; ++i) {
-        float z[16];
-        float mx = NEG_INF;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int off = i * 32 + 8 * (r >> 2) + (r & 3);
-          z[r] = off < lim ? acc[i][j][r] * p.invT : NEG_INF;
-          mx = fmaxf(mx, z[r]);
-          if (off == dt) zt_[j] = z[r];
-        }
-        const float mn = fmaxf(m_[j], mx);
-        if (mn == NEG_INF) continue;
-        const float cs = exp2f((m_[j] - mn) * LOG2E);
-        const float mb = mn * LOG2E;
-        float s = 0.0f, a = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = exp2f(__builtin_fmaf(z[r], LOG2E, -mb));
-          s += e;
-          a = __builtin_fmaf(e, z[r] == NEG_INF ? 0.0f : z[r], a);
-        }
-        s_[j] = __builtin_fmaf(s_[j], cs, s);
-        a_[j] = __builtin_fmaf(a_[j], cs, a);
-        m_[j] = mn;
-      }
-    }
+    kst = 0;
+    ++vb;
   }
 
   // combine the two lane halves (same tokens, interleaved rows), then the two vocab waves
 #pragma unroll
   for (int j = 0; j < WT; ++j) {
     const float m2 = __shfl_xor(m_[j], 32), s2 = __shfl_xor(s_[j], 32), a2 = __shfl_xor(a_[j], 32);
-    const float z2 = __shfl_xor(zt_[j], 32);
     merge(m_[j], s_[j], a_[j], m2, s2, a2);
-    if (zt_[j] != zt_[j]) zt_[j] = z2;
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // no LDS loads in flight
   __syncthreads();
-  float4* xch = reinterpret_cast<float4*>(lds);  // [2 (wt)][WT*32] states of wave wv = 1
+  static_assert(WAVES_V == 2, "the exchange below merges two vocabulary waves");
+  float4* xch = reinterpret_cast<float4*>(lds);  // [WAVES_T][WT*32] states of the waves with wv = 1
   if (wv == 1 && lane < 32) {
 #pragma unroll
-    for (int j = 0; j < WT; ++j) xch[wt * (WT * 32) + j * 32 + lane] = make_float4(m_[j], s_[j], a_[j], zt_[j]);
+    for (int j = 0; j < WT; ++j) xch[wt * (WT * 32) + j * 32 + lane] = make_float4(m_[j], s_[j], a_[j], 0.0f);
   }
   __syncthreads();
   if (wv == 0 && lane < 32) {
@@ -244,16 +321,21 @@ __global__ __launch_bounds__(NT, 1) void fused_kernel(Params p) {
     for (int j = 0; j < WT; ++j) {
       const float4 o = xch[wt * (WT * 32) + j * 32 + lane];
       merge(m_[j], s_[j], a_[j], o.x, o.y, o.z);
-      if (zt_[j] != zt_[j]) zt_[j] = o.w;
       const int n = t0 + wt * (WT * 32) + j * 32 + lane;
-      if (n < p.N) p.part[(int64_t)split * p.N + n] = make_float4(m_[j], s_[j], a_[j], zt_[j]);
+      if (n < p.N) p.part[(int64_t)split * p.N + n] = make_float4(m_[j], s_[j], a_[j], 0.0f);
     }
   }
 }
 
 struct MergeParams {
   const float4* part;
-  int N, splits;
+  const uint16_t* x;
+  int64_t xs;
+  const uint16_t* w;
+  int64_t ws;
+  const int64_t* targets;
+  int N, H, V, splits;
+  float invT;
   const float* behavior;
   float is_cap;
   float* lp;
@@ -262,16 +344,46 @@ struct MergeParams {
   int32_t* status;
 };
 
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+
+// One wave per token: the target logit z_t = (x[n] . w[t_n]) / T as an fp32 dot product,
+// the exact merge of the per-split softmax states, then log-prob, entropy, the Token-TIS
+// weight and status.
 __global__ __launch_bounds__(256) void merge_kernel(MergeParams q) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= q.N) return;
-  float m = NEG_INF, s = 0.0f, a = 0.0f, zt = __builtin_nanf("");
-  for (int k = 0; k < q.splits; ++k) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= q.N) return;  // uniform per wave
+  const int64_t t = q.targets[n];
+  float zt = __builtin_nanf("");
+  if (t >= 0 && t < q.V) {
+    const uint4* xr = reinterpret_cast<const uint4*>(q.x + (int64_t)n * q.xs);
+    const uint4* wr = reinterpret_cast<const uint4*>(q.w + t * q.ws);
+    float d0 = 0.0f, d1 = 0.0f;
+    for (int c = lane; c < q.H / 8; c += 64) {
+      const uint4 xv = xr[c], wv = wr[c];
+      d0 = __builtin_fmaf(bf16_lo(xv.x), bf16_lo(wv.x), d0);
+      d1 = __builtin_fmaf(bf16_hi(xv.x), bf16_hi(wv.x), d1);
+      d0 = __builtin_fmaf(bf16_lo(xv.y), bf16_lo(wv.y), d0);
+      d1 = __builtin_fmaf(bf16_hi(xv.y), bf16_hi(wv.y), d1);
+      d0 = __builtin_fmaf(bf16_lo(xv.z), bf16_lo(wv.z), d0);
+      d1 = __builtin_fmaf(bf16_hi(xv.z), bf16_hi(wv.z), d1);
+      d0 = __builtin_fmaf(bf16_lo(xv.w), bf16_lo(wv.w), d0);
+      d1 = __builtin_fmaf(bf16_hi(xv.w), bf16_hi(wv.w), d1);
+    }
+    zt = wave_sum(d0 + d1) * q.invT;
+  }
+  float m = NEG_INF, s = 0.0f, a = 0.0f;
+  for (int k = lane; k < q.splits; k += 64) {
     const float4 o = q.part[(int64_t)k * q.N + n];
     merge(m, s, a, o.x, o.y, o.z);
-    if (zt != zt) zt = o.w;
   }
-  const float lse = m + logf(s);
+  const float mx = wave_max(m);
+  const float c = m == NEG_INF ? 0.0f : exp2f((m - mx) * LOG2E);
+  s = wave_sum(s * c);
+  a = wave_sum(a * c);
+  if (lane != 0) return;
+  const float lse = mx + logf(s);
   const float lp = zt - lse;
   const float ent = lse - a / s;
   int st = 0;
@@ -290,7 +402,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams q) {
 }
 
 struct Plan {
-  int splits, vb_per_split, n_vb, n_tb, group_t, group_s;
+  int splits, n_vb, n_tb, group_t, group_s;
   size_t workspace;
 };
 
@@ -316,15 +428,14 @@ int plan(const dsv41_logprob_desc* d, Plan* pl) {
     return fail(DSV41_E_INVALID, "x, w, targets and out_logprob are required");
   pl->n_vb = (d->vocab + BV - 1) / BV;
   pl->n_tb = (d->n_tokens + BT - 1) / BT;
-  // about four workgroups per CU across the machine, at least one vocabulary block each
-  const int want = pl->n_tb > 0 ? (1024 + pl->n_tb - 1) / pl->n_tb : 1;
+  // one workgroup per CU: split the vocabulary so token blocks x splits fills the
+  // machine, at least one vocabulary block per split (ranges are spread evenly)
+  const int want = pl->n_tb > 0 ? std::max(1, CU_COUNT / pl->n_tb) : 1;
   pl->splits = std::max(1, std::min(want, pl->n_vb));
-  pl->vb_per_split = (pl->n_vb + pl->splits - 1) / pl->splits;
-  pl->splits = (pl->n_vb + pl->vb_per_split - 1) / pl->vb_per_split;
   // XCD super tiles of 32 workgroups (token blocks x splits) when the grid tiles
   pl->group_t = 0;
   pl->group_s = 0;
-  for (int gs : {8, 4, 16, 2, 32}) {
+  for (int gs : {4, 8, 2, 16, 1, 32}) {
     const int gt = 32 / gs;
     if (pl->splits % gs == 0 && pl->n_tb % gt == 0 && (pl->n_tb * pl->splits) % (8 * 32) == 0) {
       pl->group_t = gt;
@@ -369,7 +480,6 @@ extern "C" int dsv41_logprob_run(const dsv41_logprob_desc* d, void* workspace, s
   p.V = d->vocab;
   p.invT = 1.0f / d->temperature;
   p.splits = pl.splits;
-  p.vb_per_split = pl.vb_per_split;
   p.n_vb = pl.n_vb;
   p.n_tb = pl.n_tb;
   p.group_t = pl.group_t;
@@ -378,15 +488,23 @@ extern "C" int dsv41_logprob_run(const dsv41_logprob_desc* d, void* workspace, s
   DSV41_HIP_CHECK(hipGetLastError());
   MergeParams q{};
   q.part = p.part;
+  q.x = p.x;
+  q.xs = p.xs;
+  q.w = p.w;
+  q.ws = p.ws;
+  q.targets = d->targets;
   q.N = d->n_tokens;
+  q.H = d->hidden;
+  q.V = d->vocab;
   q.splits = pl.splits;
+  q.invT = p.invT;
   q.behavior = d->behavior;
   q.is_cap = d->is_cap;
   q.lp = d->out_logprob;
   q.ent = d->out_entropy;
   q.ratio = d->out_ratio;
   q.status = d->out_status;
-  hipLaunchKernelGGL(merge_kernel, dim3((d->n_tokens + 255) / 256), dim3(256), 0, s, q);
+  hipLaunchKernelGGL(merge_kernel, dim3((d->n_tokens + 3) / 4), dim3(256), 0, s, q);
   DSV41_HIP_CHECK(hipGetLastError());
   return DSV41_OK;
 }
