@@ -20,15 +20,17 @@
 // cache line of every row, so each line crosses L2 -> L1 once (with half-line stages
 // every line crosses twice, as the L1 cannot keep the other half until the next stage).
 // The stage sequence runs straight across vocabulary blocks, so the pipeline never
-// drains between blocks.  Each stage has two barriers: one at its start, after which the
-// other buffer is free and the next stage's loads go out, and one before its last
-// k-step, after which the next stage has landed and its first fragments are read while
-// that k-step multiplies.  MFMA operand fragments alternate between two register sets,
-// so the next k-step's reads never wait for the current k-step's multiplies.  Each
-// 128-byte LDS row holds its eight 16-byte chunks XOR-swizzled by (row >> 1) & 7; with
-// that, a wave-wide 16-byte read of one chunk of 32 consecutive rows is free of bank
-// conflicts on gfx950's LDS (measured: 4 cycles per read, against 8 for row & 7 and 32
-// unswizzled).
+// drains between blocks.  Each stage has one barrier, after its third k-step: before it
+// every wave waits for its own fragment reads of the stage and its own loads of the next
+// stage, so after it the next stage is readable by all and the current stage's buffer
+// takes the loads of the stage after next, a whole stage ahead of their use.  Those loads
+// and the next stage's first fragment reads are slotted between the multiplies of the
+// last k-step; the other k-steps carry the fragment reads of the k-step after them.  MFMA
+// operand fragments alternate between two register sets, so reads never wait for the
+// multiplies that use the other set.  Each 128-byte LDS row holds its eight 16-byte
+// chunks XOR-swizzled by (row >> 1) & 7; with that, a wave-wide 16-byte read of one chunk
+// of 32 consecutive rows is free of bank conflicts on gfx950's LDS (measured: 4 cycles per
+// read, against 8 for row & 7 and 32 unswizzled).
 
 #include <math.h>
 
@@ -128,12 +130,21 @@ __device__ __forceinline__ void read_frags(const unsigned char* stage, int addr_
   for (int j = 0; j < WT; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(stage + addr_b + j * 32 * ROWB);
 }
 
-// One k-step of the wave's WV x WT block of 32x32 outputs.
-__device__ __forceinline__ void mfma_set(floatx16 (&acc)[WV][WT], const bf16x8 (&fa)[WV], const bf16x8 (&fb)[WT]) {
+// One k-step of the wave's WV x WT block of 32x32 outputs, with other work slotted
+// between the multiplies: after multiply i,
+// extra(i) issues one fragment read or load (each group is fenced so the scheduler
+// keeps the interleave).
+template <class Extra>
+__device__ __forceinline__ void mfma_set_x(floatx16 (&acc)[WV][WT], const bf16x8 (&fa)[WV], const bf16x8 (&fb)[WT],
+                                           Extra&& extra) {
 #pragma unroll
   for (int i = 0; i < WV; ++i)
 #pragma unroll
-    for (int j = 0; j < WT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < WT; ++j) {
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      extra(i * WT + j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 // Folds one vocabulary block into the running (max z, sum e, sum e*z) of token column j.
@@ -210,27 +221,44 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     return rsrc(p.w + (int64_t)v0 * p.ws, (uint32_t)(min(BV, p.V - v0) * p.ws * 2));
   };
   __amdgpu_buffer_rsrc_t rw_ld = w_rsrc(vb0);
-  auto issue_next = [&]() {
-    unsigned char* base = lds + (ld & 1) * STAGE_BYTES;
+  // The loads of one stage, one instruction per call q = 0 .. A_LOADS + B_LOADS - 1;
+  // advance() moves to the next stage afterwards.
+  uint32_t c0 = 0, c1 = 0;
+  unsigned char* ld_base = lds;
+  auto stage_setup = [&]() {
+    ld_base = lds + (ld & 1) * STAGE_BYTES;
     const int k0 = ld_k * BK;
-    uint32_t c0 = (uint32_t)((k0 + 8 * lch) * 2), c1 = (uint32_t)((k0 + 8 * (lch ^ 4)) * 2);
+    c0 = (uint32_t)((k0 + 8 * lch) * 2);
+    c1 = (uint32_t)((k0 + 8 * (lch ^ 4)) * 2);
     if (k0 + BK > p.H) {
       c0 |= (uint32_t)(k0 + 8 * lch >= p.H) << 31;
       c1 |= (uint32_t)(k0 + 8 * (lch ^ 4) >= p.H) << 31;
     }
-#pragma unroll
-    for (int q = 0; q < A_LOADS; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw_ld, (lds_ptr_t)(base + (wid * R + q * 8) * ROWB), 16,
+    if (ld >= total) {  // past the last stage: read nothing
+      c0 |= 1u << 31;
+      c1 |= 1u << 31;
+    }
+  };
+  auto issue_one = [&](int q) {
+    if (q < A_LOADS)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw_ld, (lds_ptr_t)(ld_base + (wid * R + q * 8) * ROWB), 16,
                                                la + q * qa + ((q & 1) ? c1 : c0), 0, 0, 0);
-#pragma unroll
-    for (int q = 0; q < B_LOADS; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + (BV + wid * R + q * 8) * ROWB), 16,
-                                               lb + q * qb + ((q & 1) ? c1 : c0), 0, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(ld_base + (BV + wid * R + (q - A_LOADS) * 8) * ROWB),
+                                               16, lb + (q - A_LOADS) * qb + (((q - A_LOADS) & 1) ? c1 : c0), 0, 0, 0);
+  };
+  auto advance = [&]() {
     ++ld;
     if (++ld_k == nst) {
       ld_k = 0;
       if (++ld_vb < vb1) rw_ld = w_rsrc(ld_vb);
     }
+  };
+  auto issue_next = [&]() {
+    stage_setup();
+#pragma unroll
+    for (int q = 0; q < A_LOADS + B_LOADS; ++q) issue_one(q);
+    advance();
   };
 
   // Fragment reads: lane l takes row l%32 of each 32-row block and 8 values of chunk
@@ -241,16 +269,26 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) fch[ks] = ((2 * ks + half) ^ swz(r32)) << 4;
 
-  // prologue: stage 0 landed and its first fragments in registers
+  // Prologue: stage 0 landed, its first fragments in registers, stage 1 on its way.
   issue_next();
   wait_loads();
   barrier();
-  // two fragment sets, alternating between k-steps so that the next k-step's reads land
-  // in the set the current k-step does not use (no register copies)
   static_assert(KS == 4, "the stage body below is written for four k-steps");
+  static_assert(A_LOADS + B_LOADS <= WV * WT && WV + WT <= WV * WT, "interleave slots");
   bf16x8 fa0[WV], fb0[WT], fa1[WV], fb1[WT];
   read_frags(lds, fa_base + fch[0], fb_base + fch[0], fa0, fb0);
+  issue_next();
 
+  // One barrier per stage.  Before it every wave has all of its reads of stage st back
+  // and its loads of stage st+1 landed, so after it stage st+1 is readable and the
+  // buffer of stage st takes the loads of stage st+2, a whole stage ahead of their use.
+  // Slot order: both token fragments first, then the weight fragments, so that each read
+  // is at least six multiplies ahead of its first use in the next k-step (multiplies run
+  // i-major: fb[0], fb[1] and fa[0] are needed first).
+  auto frag_read = [&](const unsigned char* stage, int c, bf16x8 (&fa)[WV], bf16x8 (&fb)[WT], int slot) {
+    if (slot < WT) fb[slot] = *reinterpret_cast<const bf16x8*>(stage + fb_base + c + slot * 32 * ROWB);
+    else if (slot < WV + WT) fa[slot - WT] = *reinterpret_cast<const bf16x8*>(stage + fa_base + c + (slot - WT) * 32 * ROWB);
+  };
   int st = 0;  // index of the stage being multiplied in this workgroup's sequence
   for (int vb = vb0; vb < vb1; ++vb) {
     floatx16 acc[WV][WT];
@@ -260,33 +298,21 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
       for (int j = 0; j < WT; ++j) acc[i][j] = floatx16{};
     for (int kst = 0; kst < nst; ++kst, ++st) {
       const unsigned char* stage = lds + (st & 1) * STAGE_BYTES;
-      // every wave is done with stage st-1, so its buffer takes stage st+1
+      mfma_set_x(acc, fa0, fb0, [&](int i) { frag_read(stage, fch[1], fa1, fb1, i); });
+      mfma_set_x(acc, fa1, fb1, [&](int i) { frag_read(stage, fch[2], fa0, fb0, i); });
+      mfma_set_x(acc, fa0, fb0, [&](int i) { frag_read(stage, fch[3], fa1, fb1, i); });
+      __builtin_amdgcn_s_waitcnt(0);  // own reads of stage st back, own loads of stage st+1 landed
       barrier();
-      if (ld < total) issue_next();
-      // The scheduling fences keep each k-step's reads ahead of the other set's
-      // multiplies (left alone, the scheduler sinks them between the multiplies to reuse
-      // registers, and the multiplies that follow then wait for LDS latency).
-      read_frags(stage, fa_base + fch[1], fb_base + fch[1], fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_set(acc, fa0, fb0);
-      __builtin_amdgcn_sched_barrier(0);
-      read_frags(stage, fa_base + fch[2], fb_base + fch[2], fa0, fb0);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_set(acc, fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      read_frags(stage, fa_base + fch[3], fb_base + fch[3], fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_set(acc, fa0, fb0);
-      __builtin_amdgcn_sched_barrier(0);
-      // Stage st+1 has landed for every wave after this barrier.  After the last stage the
-      // reads below fetch a buffer nobody uses; they stay unconditional so the LDS-read
-      // counter waits of the multiplies below see one straight-line sequence.
-      wait_loads();
-      barrier();
-      read_frags(lds + ((st + 1) & 1) * STAGE_BYTES, fa_base + fch[0], fb_base + fch[0], fa0, fb0);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_set(acc, fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
+      const unsigned char* next = lds + ((st + 1) & 1) * STAGE_BYTES;
+      // After the last stage the reads below fetch a buffer nobody uses and the loads
+      // read zeros (offsets past the buffer); both stay unconditional so the multiplies
+      // see one straight-line sequence.
+      stage_setup();
+      mfma_set_x(acc, fa1, fb1, [&](int i) {
+        frag_read(next, fch[0], fa0, fb0, i);
+        if (i < A_LOADS + B_LOADS) issue_one(i);
+      });
+      advance();
     }
 
     // end of a vocabulary block: lane holds rows 8*(r/4) + 4*(lane/32) + r%4 of each
