@@ -1029,6 +1029,130 @@ __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, cons
   return keep;
 }
 
+// Descending sort of 64*R u64 keys held by one wave, key at position r*64 + lane in
+// k[r], by the bitonic network (stride >= 64: within the lane; below: lane exchange).
+template <int R>
+__device__ __forceinline__ void wave_sort_desc(uint64_t (&k)[R], int lane) {
+  constexpr int N = 64 * R;
+#pragma unroll
+  for (int s = 2; s <= N; s <<= 1) {
+#pragma unroll
+    for (int j = s >> 1; j > 0; j >>= 1) {
+      if (j >= 64) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int pr = r ^ (j >> 6);
+          if (pr > r) {
+            const bool desc = ((r * 64) & s) == 0;  // block direction (s >= 128: lane bits do not matter)
+            const uint64_t a = k[r], b = k[pr];
+            const bool sw = desc ? (a < b) : (a > b);
+            k[r] = sw ? b : a;
+            k[pr] = sw ? a : b;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint64_t o = __shfl_xor(k[r], j);
+          const bool desc = ((r * 64 + lane) & s) == 0;
+          const bool lower = (lane & j) == 0;
+          const bool take_max = lower == desc;
+          k[r] = take_max ? (k[r] > o ? k[r] : o) : (k[r] < o ? k[r] : o);
+        }
+      }
+    }
+  }
+}
+
+// Inclusive prefix of x over positions r*64 + lane; returns the total.
+template <int R>
+__device__ __forceinline__ uint64_t wave_prefix(const uint64_t (&x)[R], uint64_t (&incl)[R], int lane) {
+  uint64_t carry = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    incl[r] = wave_incl_scan_u64(x[r], lane) + carry;
+    carry = __shfl(incl[r], 63);
+  }
+  return carry;
+}
+
+// Final selection of the TOPK kernel by one wave when 1 <= n <= 64*R candidates: the
+// same decisions as the workgroup path (min-p, top-k, top-p over exact integer masses,
+// inverse-CDF draw in vocabulary order), with every step in registers.
+template <int R>
+__device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, const uint64_t* cand, int n, float u) {
+  const int lane = threadIdx.x & 63;
+  uint64_t k[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) k[r] = r * 64 + lane < n ? cand[r * 64 + lane] : 0;  // 0 is below every key
+  wave_sort_desc<R>(k, lane);
+  const uint64_t k0 = __shfl(k[0], 0);
+  const float zmax = ckey_z(k0);
+  int el = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    el += (int)__popcll(__ballot(r * 64 + lane < n && minp_ok(ckey_z(k[r]), zmax, p)));
+  const int K = min(p.top_k, el);
+  uint64_t q[R], pre[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) q[r] = r * 64 + lane < K ? mass_of(ckey_z(k[r]), zmax) : 0;
+  const uint64_t SK = wave_prefix<R>(q, pre, lane);
+  int n_keep = K;
+  uint64_t S = SK;
+  if (p.top_p < 1.0f) {
+    const uint64_t thr = top_p_threshold(p.top_p, SK);
+    int first = -1;
+#pragma unroll
+    for (int r = R - 1; r >= 0; --r) {
+      const unsigned long long b = __ballot(r * 64 + lane < K && pre[r] >= thr);
+      if (b) {
+        first = r * 64 + (int)__builtin_ctzll(b);
+        S = __shfl(pre[r], first & 63);
+      }
+    }
+    if (first < 0) {  // unreachable: the total reaches every threshold
+      first = K - 1;
+      S = SK;
+    }
+    n_keep = first + 1;
+  }
+  double es = 0.0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r * 64 + lane < n_keep) es += exp_det((double)ckey_z(k[r]) - (double)zmax);
+  const double esum = wave_sum_d(es);
+  int64_t tok = (int64_t)ckey_idx(k0);
+  float ztok = zmax;
+  if (!p.greedy) {
+    // kept candidates in vocabulary order: ~(index, z) sorts descending as index ascending
+    uint64_t k2[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      k2[r] = r * 64 + lane < n_keep ? ~(((uint64_t)ckey_idx(k[r]) << 32) | (k[r] >> 32)) : 0;
+    wave_sort_desc<R>(k2, lane);
+    const uint64_t t = draw_target(u, S);
+    uint64_t w[R], cum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = r * 64 + lane < n_keep ? mass_of(okey_inv((uint32_t)~k2[r]), zmax) : 0;
+    wave_prefix<R>(w, cum, lane);
+    bool done = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const unsigned long long b = __ballot(r * 64 + lane < n_keep && cum[r] > t);
+      if (b && !done) {
+        const uint64_t key = ~__shfl(k2[r], (int)__builtin_ctzll(b));
+        tok = (int64_t)(key >> 32);
+        ztok = okey_inv((uint32_t)key);
+        done = true;
+      }
+    }
+  }
+  if (lane == 0) {
+    const float lp = (float)(((double)ztok - (double)zmax) - log(esum));
+    write_result(p, row, m, tok, lp, n_keep);
+  }
+}
+
 template <typename TIn, bool VEC>
 __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   constexpr int NT = TOPK_NT, NW = NT / 64, G = TOPK_G, TILE = TOPK_TILE, HR = 8;
@@ -1244,8 +1368,17 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
 
-  // final selection over the candidates
+  // final selection over the candidates: one wave when they fit its registers
   const int n = count;
+  if (n >= 1 && n <= 4 * 64) {
+    if (wid == 0) {
+      const float u = row_uniform(p, row, m);
+      if (n <= 64) wave_final<1>(p, row, m, cand, n, u);
+      else if (n <= 128) wave_final<2>(p, row, m, cand, n, u);
+      else wave_final<4>(p, row, m, cand, n, u);
+    }
+    return;
+  }
   bitonic_sort_desc<NT>(cand, n);
   const float u = row_uniform(p, row, m);
   if (n == 0) {  // only possible for rows without a finite maximum
