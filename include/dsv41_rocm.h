@@ -18,6 +18,10 @@
  *   dsv41_logprob_run  <- dsv41_train/models/dsv4/model.py:679-684 (_token_log_probs),
  *                         dsv41_train/rl/native_lora.py:80-82 (_score_targets),
  *                         plus the Token-TIS weight of dsv41_train/rl/algorithm.py:293-299.
+ *   dsv41_logprob_grad_run <- the autograd backward of that expression as the learner
+ *                         differentiates it (dsv41_train/rl/distributed_grpo.py:352-375 over
+ *                         native_lora.py:120-122 / model.py:735-738): the gradient with
+ *                         respect to the lm_head output, in that output's dtype (bf16).
  */
 #ifndef DSV41_ROCM_H
 #define DSV41_ROCM_H
@@ -29,7 +33,7 @@
 extern "C" {
 #endif
 
-#define DSV41_ABI_VERSION 1
+#define DSV41_ABI_VERSION 2
 
 /* Element types of logits / activations. */
 #define DSV41_DTYPE_F32 0
@@ -116,12 +120,47 @@ typedef struct dsv41_logprob_desc {
   float* out_entropy;     /* [N] or NULL */
   float* out_ratio;       /* [N] or NULL; requires behavior */
   int32_t* out_status;    /* [N] or NULL */
+  float* out_lse;         /* [N] or NULL: logsumexp(z[n, :]), kept for the backward */
 } dsv41_logprob_desc;
+
+/*
+ * Gradient of a loss L(out_logprob, out_entropy) with respect to the logits, for the
+ * vocabulary rows [vocab_begin, vocab_end):
+ *   p = softmax(z[n]),  z = logits / temperature,
+ *   dL/dz[n, v] = grad_logprob[n] * ([v == targets[n]] - p[n, v])
+ *               + grad_entropy[n] * p[n, v] * (lse[n] - entropy[n] - z[n, v])
+ *   out[n, v - vocab_begin] = bf16(dL/dz[n, v] / temperature)        (round to nearest even)
+ * with lse and entropy as written by dsv41_logprob_run.  NULL grad_logprob or grad_entropy
+ * counts as zero.  The logits are recomputed on the matrix cores, never stored in fp32.
+ * dL/dx = out @ w[vocab_begin:vocab_end] and dL/dw[vocab_begin:vocab_end] = out^T @ x are
+ * plain GEMMs left to the caller's BLAS.
+ */
+typedef struct dsv41_logprob_grad_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_logprob_grad_desc) */
+  int32_t n_tokens;
+  int32_t hidden;
+  int32_t vocab;            /* rows of w */
+  const void* x;            /* bf16 [N, H] */
+  int64_t x_row_stride;     /* in elements, multiple of 8 */
+  const void* w;            /* bf16 [V, H] */
+  int64_t w_row_stride;     /* in elements, multiple of 8 */
+  const int64_t* targets;   /* [N], each in [0, V) */
+  float temperature;        /* finite, > 0; the forward's */
+  const float* lse;         /* [N] */
+  const float* entropy;     /* [N]; required when grad_entropy != NULL */
+  const float* grad_logprob; /* [N] or NULL */
+  const float* grad_entropy; /* [N] or NULL */
+  int32_t vocab_begin;      /* 0 <= vocab_begin < vocab_end <= vocab */
+  int32_t vocab_end;
+  void* out;                /* bf16 [N, out_row_stride] */
+  int64_t out_row_stride;   /* in elements, >= vocab_end - vocab_begin, multiple of 8 */
+} dsv41_logprob_grad_desc;
 
 /* ABI identity. */
 int dsv41_abi_version(void);
 size_t dsv41_sampler_desc_size(void);
 size_t dsv41_logprob_desc_size(void);
+size_t dsv41_logprob_grad_desc_size(void);
 const char* dsv41_last_error(void);
 
 /* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch. */
@@ -133,6 +172,9 @@ int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t wo
 size_t dsv41_logprob_workspace_bytes(const dsv41_logprob_desc* desc);
 int dsv41_logprob_run(const dsv41_logprob_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream /* hipStream_t */);
+
+/* Gradient of the fused log-prob with respect to the logits (no workspace). */
+int dsv41_logprob_grad_run(const dsv41_logprob_grad_desc* desc, void* stream /* hipStream_t */);
 
 #ifdef __cplusplus
 }

@@ -9,7 +9,7 @@ TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
   restatement of ``dsv41_train/rl/rollout.py:144-150`` plus the vLLM knobs.
 * ``logprob_oracle`` (numpy fp64) restates ``dsv41_train/models/dsv4/model.py:679-684``,
   ``dsv41_train/rl/native_lora.py:80-82`` and the Token-TIS weight of
-  ``dsv41_train/rl/algorithm.py:293-299``.
+  ``dsv41_train/rl/algorithm.py:293-299``; ``logprob_grad_oracle`` its backward.
 
 Pinning: tests/test_oracle_sampler.py and tests/test_oracle_logprob.py check every
 function here against closed forms, brute force on tiny inputs, libm, torch and the
@@ -25,7 +25,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .logprob_oracle import logprob_oracle, token_tis_weight  # noqa: F401
+from .logprob_oracle import logprob_grad_oracle, logprob_oracle, token_tis_weight  # noqa: F401
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle_dsv41.so"

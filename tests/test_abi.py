@@ -33,7 +33,8 @@ def test_library_exports_every_declared_function():
 
 
 def test_descriptor_layouts_match_header(tmp_path):
-    fields = {"dsv41_sampler_desc": _lib.SamplerDesc, "dsv41_logprob_desc": _lib.LogprobDesc}
+    fields = {"dsv41_sampler_desc": _lib.SamplerDesc, "dsv41_logprob_desc": _lib.LogprobDesc,
+              "dsv41_logprob_grad_desc": _lib.LogprobGradDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {", 'printf("{");']
     first = True
     for cname, cls in fields.items():
@@ -131,6 +132,39 @@ def test_logprob_workspace_and_empty_batch():
     assert lib.dsv41_logprob_run(ctypes.byref(empty), None, 0, None) == _lib.OK
 
 
+def _grad_desc(**kw):
+    d = _lib.LogprobGradDesc()
+    d.struct_size = ctypes.sizeof(_lib.LogprobGradDesc)
+    d.n_tokens, d.hidden, d.vocab = 10, 64, 300
+    d.x, d.x_row_stride, d.w, d.w_row_stride = 0x1000, 64, 0x2000, 64
+    d.targets, d.lse, d.temperature = 0x3000, 0x4000, 1.0
+    d.vocab_begin, d.vocab_end, d.out, d.out_row_stride = 0, 300, 0x5000, 304
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(temperature=0.0), _lib.E_INVALID, "temperature must be finite and positive"),
+    (dict(vocab_begin=10, vocab_end=10), _lib.E_INVALID, "vocabulary range"),
+    (dict(vocab_end=301), _lib.E_INVALID, "vocabulary range"),
+    (dict(out_row_stride=296), _lib.E_INVALID, "output row stride"),
+    (dict(out_row_stride=302), _lib.E_INVALID, "output row stride"),
+    (dict(out=0x5008), _lib.E_INVALID, "aligned"),
+    (dict(grad_entropy=0x6000), _lib.E_INVALID, "entropies"),
+    (dict(lse=None), _lib.E_INVALID, "lse"),
+    (dict(hidden=60, x_row_stride=64, w_row_stride=64), _lib.E_UNSUPPORTED, "multiple of 8"),
+    (dict(struct_size=16), _lib.E_ABI, "size mismatch"),
+])
+def test_logprob_grad_rejects_bad_descriptors_before_launch(kw, code, msg):
+    lib = _lib.load()
+    d = _grad_desc(**kw)
+    assert lib.dsv41_logprob_grad_run(ctypes.byref(d), None) == code
+    assert msg in _lib.last_error()
+    empty = _grad_desc(n_tokens=0)
+    assert lib.dsv41_logprob_grad_run(ctypes.byref(empty), None) == _lib.OK
+
+
 def test_python_entry_points_fail_loudly_off_gpu():
     with pytest.raises(ValueError, match="GPU"):
         sample(torch.zeros(2, 10))
@@ -157,9 +191,9 @@ def test_custom_ops_registered_with_fake_kernels():
         h = torch.empty(5, 16, dtype=torch.bfloat16, device="meta")
         w = torch.empty(30, 16, dtype=torch.bfloat16, device="meta")
         t = torch.empty(5, dtype=torch.int64, device="meta")
-        lp, ent, ratio = torch.ops.dsv41_rocm.selected_log_probs(h, w, t, 1.0, None, 2.0)
-        assert lp.shape == ent.shape == (5,) and ratio.shape == (0,)
-        lp, ent, ratio = torch.ops.dsv41_rocm.selected_log_probs(h, w, t, 1.0, torch.empty(5, device="meta"), 2.0)
+        lp, ent, ratio, lse = torch.ops.dsv41_rocm.selected_log_probs(h, w, t, 1.0, None, 2.0)
+        assert lp.shape == ent.shape == lse.shape == (5,) and ratio.shape == (0,)
+        lp, ent, ratio, _ = torch.ops.dsv41_rocm.selected_log_probs(h, w, t, 1.0, torch.empty(5, device="meta"), 2.0)
         assert ratio.shape == (5,)
 
 

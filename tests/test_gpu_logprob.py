@@ -125,8 +125,10 @@ def test_custom_op_matches_wrapper():
     x, w, t = inp["x"], inp["w"], inp["targets"]
     print("case: torch.ops.dsv41_rocm.selected_log_probs on config C, 64 tokens", flush=True)
     behavior = torch.full((64,), -12.0, device=DEV)
-    lp, ent, ratio = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, behavior, 2.0)
+    lp, ent, ratio, lse = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, behavior, 2.0)
     rlp, rent, rratio = selected_log_probs(x, w, t, 0.9, behavior=behavior, is_cap=2.0)
     assert torch.equal(lp, rlp) and torch.equal(ent, rent) and torch.equal(ratio, rratio)
-    lp2, _, empty = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, None, 2.0)
+    zt = (x.double() * w[t].double()).sum(-1) / 0.9
+    assert torch.max(torch.abs(lse.double() - (zt - lp.double()))).item() <= 1e-4
+    lp2, _, empty, _ = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, None, 2.0)
     assert torch.equal(lp2, rlp) and empty.numel() == 0

@@ -63,3 +63,32 @@ def test_token_tis_weight_known_answers_from_reference_tests():
             assert abs(w.min() - c["is_weight_min"]) < 1e-6 and w.max() == c["is_weight_max"]
         if "is_clipped_fraction" in c:
             assert (raw > c["is_cap"]).mean() == c["is_clipped_fraction"]
+
+
+def test_grad_oracle_matches_torch_fp64_autograd():
+    """The backward restatement against torch autograd of the reference expression in fp64
+    (log_softmax(x @ w.T / T).gather, entropy = -(p * log p).sum), with both upstream
+    gradients nonzero and a token whose target is the row maximum."""
+    x = _bf16_values((23, 40), 1.0, 11)
+    w = _bf16_values((301, 40), 0.4, 12)
+    rng = np.random.default_rng(13)
+    t = rng.integers(0, 301, 23)
+    glp = rng.normal(size=23)
+    gent = rng.normal(size=23)
+    for T in (1.0, 0.6):
+        gl, dx, dw = oracle.logprob_grad_oracle(x, w, t, T, glp, gent, chunk=7)
+        xt = torch.from_numpy(x).double().requires_grad_()
+        wt = torch.from_numpy(w).double().requires_grad_()
+        logits = xt @ wt.T
+        logits.retain_grad()
+        lsm = torch.log_softmax(logits / T, -1)
+        lp = lsm.gather(-1, torch.from_numpy(t)[:, None])[:, 0]
+        ent = -(lsm.exp() * lsm).sum(-1)
+        ((torch.from_numpy(glp) * lp).sum() + (torch.from_numpy(gent) * ent).sum()).backward()
+        np.testing.assert_allclose(gl, logits.grad.numpy(), atol=1e-12)
+        np.testing.assert_allclose(dx, xt.grad.numpy(), atol=1e-10)
+        np.testing.assert_allclose(dw, wt.grad.numpy(), atol=1e-10)
+    # log-prob alone: each logit-gradient row sums to zero and equals (onehot - softmax) / T
+    gl, _, _ = oracle.logprob_grad_oracle(x, w, t, 0.8, np.ones(23))
+    np.testing.assert_allclose(gl.sum(axis=1), 0.0, atol=1e-12)
+    assert np.all(gl[np.arange(23), t] > 0) and np.all(np.delete(gl[0], t[0]) < 0)

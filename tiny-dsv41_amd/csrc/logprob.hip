@@ -52,6 +52,8 @@ constexpr int KS = BK / 16;                  // MFMA k-steps per stage
 constexpr int ROWB = BK * 2;                 // bytes per LDS row: one 128-byte cache line
 constexpr int STAGE_BYTES = (BV + BT) * ROWB;  // 64 KiB
 constexpr int LDS_BYTES = 2 * STAGE_BYTES;   // two stage buffers
+constexpr int GROW = BV * 2 + 16;            // bytes per token row of the backward's staged bf16 tile
+constexpr int GRAD_LDS = BT * GROW > LDS_BYTES ? BT * GROW : LDS_BYTES;
 constexpr int ROWS_PER_LOAD = 1024 / ROWB;   // rows one wave-wide 16-byte LDS load fills
 constexpr int A_LOADS = BV / NWAVES / ROWS_PER_LOAD;  // per wave per stage
 constexpr int B_LOADS = BT / NWAVES / ROWS_PER_LOAD;
@@ -67,14 +69,22 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 struct Params {
   const uint16_t* x;
   int64_t xs;
-  const uint16_t* w;
+  const uint16_t* w;  // (backward: row vbeg of the head)
   int64_t ws;
   const int64_t* targets;
   float4* part;  // [splits][N] (max z, sum e, sum e*z, unused)
-  int N, H, V;
+  int N, H, V;   // (backward: V = rows of the vocabulary range)
   float invT;
   int splits, n_vb, n_tb;
   int group_t, group_s;  // XCD super-tile shape (0: linear mapping)
+  // backward only
+  const float* lse;
+  const float* ent;
+  const float* glp;
+  const float* gent;
+  uint16_t* out;  // bf16 [N, os]
+  int64_t os;
+  int vbeg;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
@@ -181,8 +191,76 @@ __device__ __forceinline__ void absorb(const floatx16 (&acc)[WV][WT], int j, int
   m = mn;
 }
 
+// Two floats to bf16 (round to nearest even), packed low | high << 16.
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Backward epilogue of one 256 x 256 block: dL/dz per element from the recomputed logit,
+// scaled by 1/T and rounded to bf16, staged transposed in LDS (token rows of GROW bytes)
+// and written out as 16-byte pieces of output rows.
+__device__ __forceinline__ void grad_block(const Params& p, unsigned char* lds, const floatx16 (&acc)[WV][WT],
+                                           int t0, int vb, int wv, int wt, int lane) {
+  const int tid = threadIdx.x, r32 = lane & 31, half = lane >> 5;
+  __builtin_amdgcn_s_waitcnt(0);  // every load of this wave landed (also the zero loads past the end)
+  __syncthreads();                // and every wave's: the stage buffers are free
+#pragma unroll
+  for (int j = 0; j < WT; ++j) {
+    const int nl = wt * (WT * 32) + j * 32 + r32;
+    const int n = t0 + nl;
+    float lse = 0.0f, glp = 0.0f, gent = 0.0f, cent = 0.0f;
+    int tl = -1;  // target row within this block, if there
+    if (n < p.N) {
+      lse = p.lse[n];
+      glp = p.glp ? p.glp[n] : 0.0f;
+      gent = p.gent ? p.gent[n] : 0.0f;
+      cent = p.gent ? lse - p.ent[n] : 0.0f;  // lse - entropy = E[z]
+      const int64_t t = p.targets[n] - p.vbeg - (int64_t)vb * BV;
+      tl = (t >= 0 && t < BV) ? (int)t : -1;
+    }
+    const float mb = lse * LOG2E, c1 = p.invT * LOG2E;
+#pragma unroll
+    for (int i = 0; i < WV; ++i)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int v0 = wv * (WV * 32) + i * 32 + 8 * g4 + 4 * half;  // rows v0 .. v0+3
+        float gv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = acc[i][j][4 * g4 + e];
+          const float z = a * p.invT;
+          const float pr = exp2f(__builtin_fmaf(a, c1, -mb));
+          const float onehot = (v0 + e == tl) ? 1.0f : 0.0f;
+          const float g = glp * (onehot - pr) + gent * pr * (cent - z);
+          gv[e] = g * p.invT;
+        }
+        uint2 w2;
+        w2.x = pack_bf16(gv[0], gv[1]);
+        w2.y = pack_bf16(gv[2], gv[3]);
+        *reinterpret_cast<uint2*>(lds + nl * GROW + v0 * 2) = w2;
+      }
+  }
+  __syncthreads();
+  const int rows = min(BT, p.N - t0), cols = min(BV, p.V - vb * BV);
+  for (int idx = tid; idx < BT * (BV / 8); idx += NT) {
+    const int nl = idx / (BV / 8), c0 = (idx % (BV / 8)) * 8;
+    if (nl >= rows || c0 >= cols) continue;
+    const uint4 val = *reinterpret_cast<const uint4*>(lds + nl * GROW + c0 * 2);
+    uint16_t* dst = p.out + (int64_t)(t0 + nl) * p.os + (int64_t)vb * BV + c0;
+    if (c0 + 8 <= cols) {
+      *reinterpret_cast<uint4*>(dst) = val;
+    } else {
+      const uint32_t wds[4] = {val.x, val.y, val.z, val.w};
+      for (int e = 0; e < cols - c0; ++e) dst[e] = (uint16_t)(wds[e >> 1] >> ((e & 1) * 16));
+    }
+  }
+}
+
+template <bool GRAD>
 __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void fused_kernel(Params p) {
-  __shared__ __align__(16) unsigned char lds[LDS_BYTES];
+  __shared__ __align__(16) unsigned char lds[GRAD ? GRAD_LDS : LDS_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wv = wid % WAVES_V, wt = wid / WAVES_V;
@@ -317,6 +395,10 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 
     // end of a vocabulary block: lane holds rows 8*(r/4) + 4*(lane/32) + r%4 of each
     // 32-row block, at offsets from rbase that are compile-time constants
+    if constexpr (GRAD) {
+      grad_block(p, lds, acc, t0, vb, wv, wt, lane);  // the backward's grid has one block per workgroup
+      continue;
+    }
     const int rbase = vb * BV + wv * (WV * 32) + 4 * half;
     if ((vb + 1) * BV <= p.V) {
 #pragma unroll
@@ -328,6 +410,7 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     }
   }
 
+  if constexpr (GRAD) return;
   // combine the two lane halves (same tokens, interleaved rows), then the two vocab waves
 #pragma unroll
   for (int j = 0; j < WT; ++j) {
@@ -369,6 +452,7 @@ struct MergeParams {
   float* ent;
   float* ratio;
   int32_t* status;
+  float* lse_out;
 };
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
@@ -417,6 +501,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams q) {
   if (!isfinite(lp) || !isfinite(ent)) st |= DSV41_STATUS_NONFINITE;
   q.lp[n] = lp;
   if (q.ent) q.ent[n] = ent;
+  if (q.lse_out) q.lse_out[n] = lse;
   if (q.ratio) {
     // algorithm.py:293-299: delta in fp32, exp in fp64, clamp at the cap, back to fp32
     const float delta = lp - q.behavior[n];
@@ -432,6 +517,20 @@ struct Plan {
   int splits, n_vb, n_tb, group_t, group_s;
   size_t workspace;
 };
+
+// XCD super tiles of 32 workgroups (token blocks x splits) when the grid tiles.
+void xcd_groups(Plan* pl) {
+  pl->group_t = 0;
+  pl->group_s = 0;
+  for (int gs : {4, 8, 2, 16, 1, 32}) {
+    const int gt = 32 / gs;
+    if (pl->splits % gs == 0 && pl->n_tb % gt == 0 && (pl->n_tb * pl->splits) % (8 * 32) == 0) {
+      pl->group_t = gt;
+      pl->group_s = gs;
+      break;
+    }
+  }
+}
 
 int plan(const dsv41_logprob_desc* d, Plan* pl) {
   if (!d) return fail(DSV41_E_INVALID, "log-prob descriptor is NULL");
@@ -459,18 +558,39 @@ int plan(const dsv41_logprob_desc* d, Plan* pl) {
   // machine, at least one vocabulary block per split (ranges are spread evenly)
   const int want = pl->n_tb > 0 ? std::max(1, CU_COUNT / pl->n_tb) : 1;
   pl->splits = std::max(1, std::min(want, pl->n_vb));
-  // XCD super tiles of 32 workgroups (token blocks x splits) when the grid tiles
-  pl->group_t = 0;
-  pl->group_s = 0;
-  for (int gs : {4, 8, 2, 16, 1, 32}) {
-    const int gt = 32 / gs;
-    if (pl->splits % gs == 0 && pl->n_tb % gt == 0 && (pl->n_tb * pl->splits) % (8 * 32) == 0) {
-      pl->group_t = gt;
-      pl->group_s = gs;
-      break;
-    }
-  }
+  xcd_groups(pl);
   pl->workspace = (size_t)pl->splits * (size_t)d->n_tokens * sizeof(float4);
+  return DSV41_OK;
+}
+
+// Backward: one workgroup per 256 x 256 block of the vocabulary range x tokens.
+int plan_grad(const dsv41_logprob_grad_desc* d, Plan* pl) {
+  if (!d) return fail(DSV41_E_INVALID, "log-prob gradient descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_logprob_grad_desc))
+    return fail(DSV41_E_ABI, "dsv41_logprob_grad_desc size mismatch (rebuild the binding)");
+  if (d->n_tokens < 0 || d->hidden <= 0 || d->vocab <= 0)
+    return fail(DSV41_E_INVALID, "hidden states must be [tokens, hidden] and the head [vocab, hidden]");
+  if (d->hidden % 8 != 0) return fail(DSV41_E_UNSUPPORTED, "hidden size must be a multiple of 8");
+  if (d->x_row_stride < d->hidden || d->w_row_stride < d->hidden || d->x_row_stride % 8 || d->w_row_stride % 8)
+    return fail(DSV41_E_INVALID, "row strides must be >= hidden and multiples of 8 elements");
+  if (((uintptr_t)d->x | (uintptr_t)d->w | (uintptr_t)d->out) % 16)
+    return fail(DSV41_E_INVALID, "hidden states, head weight and output must be 16-byte aligned");
+  if ((int64_t)BV * d->w_row_stride * 2 >= (1ll << 31) || (int64_t)BT * d->x_row_stride * 2 >= (1ll << 31))
+    return fail(DSV41_E_UNSUPPORTED, "row stride too large for 32-bit block offsets");
+  if (!(isfinite(d->temperature) && d->temperature > 0.0f))
+    return fail(DSV41_E_INVALID, "temperature must be finite and positive");
+  if (!(0 <= d->vocab_begin && d->vocab_begin < d->vocab_end && d->vocab_end <= d->vocab))
+    return fail(DSV41_E_INVALID, "vocabulary range must satisfy 0 <= begin < end <= vocab");
+  if (d->out_row_stride < d->vocab_end - d->vocab_begin || d->out_row_stride % 8)
+    return fail(DSV41_E_INVALID, "output row stride must cover the range and be a multiple of 8 elements");
+  if (d->n_tokens > 0 && (!d->x || !d->w || !d->targets || !d->lse || !d->out))
+    return fail(DSV41_E_INVALID, "x, w, targets, lse and out are required");
+  if (d->grad_entropy && !d->entropy) return fail(DSV41_E_INVALID, "an entropy gradient requires the entropies");
+  pl->n_vb = (d->vocab_end - d->vocab_begin + BV - 1) / BV;
+  pl->n_tb = (d->n_tokens + BT - 1) / BT;
+  pl->splits = pl->n_vb;
+  xcd_groups(pl);
+  pl->workspace = 0;
   return DSV41_OK;
 }
 
@@ -479,6 +599,38 @@ int plan(const dsv41_logprob_desc* d, Plan* pl) {
 
 using namespace dsv41;
 using namespace dsv41::logprob;
+
+extern "C" int dsv41_logprob_grad_run(const dsv41_logprob_grad_desc* d, void* stream) {
+  Plan pl;
+  int rc = plan_grad(d, &pl);
+  if (rc != DSV41_OK) return rc;
+  if (d->n_tokens == 0) return DSV41_OK;
+  Params p{};
+  p.x = static_cast<const uint16_t*>(d->x);
+  p.xs = d->x_row_stride;
+  p.ws = d->w_row_stride;
+  p.w = static_cast<const uint16_t*>(d->w) + (int64_t)d->vocab_begin * p.ws;
+  p.targets = d->targets;
+  p.N = d->n_tokens;
+  p.H = d->hidden;
+  p.V = d->vocab_end - d->vocab_begin;
+  p.invT = 1.0f / d->temperature;
+  p.splits = pl.splits;
+  p.n_vb = pl.n_vb;
+  p.n_tb = pl.n_tb;
+  p.group_t = pl.group_t;
+  p.group_s = pl.group_s;
+  p.lse = d->lse;
+  p.ent = d->entropy;
+  p.glp = d->grad_logprob;
+  p.gent = d->grad_entropy;
+  p.out = static_cast<uint16_t*>(d->out);
+  p.os = d->out_row_stride;
+  p.vbeg = d->vocab_begin;
+  hipLaunchKernelGGL(fused_kernel<true>, dim3(pl.n_tb * pl.splits), dim3(NT), 0, static_cast<hipStream_t>(stream), p);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
+}
 
 extern "C" size_t dsv41_logprob_workspace_bytes(const dsv41_logprob_desc* d) {
   Plan pl;
@@ -511,7 +663,7 @@ extern "C" int dsv41_logprob_run(const dsv41_logprob_desc* d, void* workspace, s
   p.n_tb = pl.n_tb;
   p.group_t = pl.group_t;
   p.group_s = pl.group_s;
-  hipLaunchKernelGGL(fused_kernel, dim3(pl.n_tb * pl.splits), dim3(NT), 0, s, p);
+  hipLaunchKernelGGL(fused_kernel<false>, dim3(pl.n_tb * pl.splits), dim3(NT), 0, s, p);
   DSV41_HIP_CHECK(hipGetLastError());
   MergeParams q{};
   q.part = p.part;
@@ -531,6 +683,7 @@ extern "C" int dsv41_logprob_run(const dsv41_logprob_desc* d, void* workspace, s
   q.ent = d->out_entropy;
   q.ratio = d->out_ratio;
   q.status = d->out_status;
+  q.lse_out = d->out_lse;
   hipLaunchKernelGGL(merge_kernel, dim3((d->n_tokens + 3) / 4), dim3(256), 0, s, q);
   DSV41_HIP_CHECK(hipGetLastError());
   return DSV41_OK;

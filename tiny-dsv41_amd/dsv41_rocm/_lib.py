@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).with_name("libdsv41hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -81,6 +81,32 @@ class LogprobDesc(ctypes.Structure):
         ("out_entropy", ctypes.c_void_p),
         ("out_ratio", ctypes.c_void_p),
         ("out_status", ctypes.c_void_p),
+        ("out_lse", ctypes.c_void_p),
+    ]
+
+
+class LogprobGradDesc(ctypes.Structure):
+    """Mirror of dsv41_logprob_grad_desc."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("n_tokens", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("x_row_stride", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("w_row_stride", ctypes.c_int64),
+        ("targets", ctypes.c_void_p),
+        ("temperature", ctypes.c_float),
+        ("lse", ctypes.c_void_p),
+        ("entropy", ctypes.c_void_p),
+        ("grad_logprob", ctypes.c_void_p),
+        ("grad_entropy", ctypes.c_void_p),
+        ("vocab_begin", ctypes.c_int32),
+        ("vocab_end", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+        ("out_row_stride", ctypes.c_int64),
     ]
 
 
@@ -88,11 +114,13 @@ EXPORTS = (
     "dsv41_abi_version",
     "dsv41_sampler_desc_size",
     "dsv41_logprob_desc_size",
+    "dsv41_logprob_grad_desc_size",
     "dsv41_last_error",
     "dsv41_sampler_workspace_bytes",
     "dsv41_sampler_run",
     "dsv41_logprob_workspace_bytes",
     "dsv41_logprob_run",
+    "dsv41_logprob_grad_run",
 )
 
 _lock = threading.Lock()
@@ -103,6 +131,7 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_abi_version.restype = ctypes.c_int
     lib.dsv41_sampler_desc_size.restype = ctypes.c_size_t
     lib.dsv41_logprob_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_logprob_grad_desc_size.restype = ctypes.c_size_t
     lib.dsv41_last_error.restype = ctypes.c_char_p
     lib.dsv41_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.dsv41_sampler_workspace_bytes.argtypes = [ctypes.POINTER(SamplerDesc)]
@@ -114,6 +143,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_logprob_run.restype = ctypes.c_int
     lib.dsv41_logprob_run.argtypes = [ctypes.POINTER(LogprobDesc), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p]
+    lib.dsv41_logprob_grad_run.restype = ctypes.c_int
+    lib.dsv41_logprob_grad_run.argtypes = [ctypes.POINTER(LogprobGradDesc), ctypes.c_void_p]
     return lib
 
 
@@ -134,6 +165,8 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("dsv41_sampler_desc layout differs between library and binding")
         if lib.dsv41_logprob_desc_size() != ctypes.sizeof(LogprobDesc):
             raise RuntimeError("dsv41_logprob_desc layout differs between library and binding")
+        if lib.dsv41_logprob_grad_desc_size() != ctypes.sizeof(LogprobGradDesc):
+            raise RuntimeError("dsv41_logprob_grad_desc layout differs between library and binding")
         _lib = lib
         return lib
 

@@ -4,7 +4,10 @@
 
 * ``dsv41_rocm::sample_rows`` — the row sampler; returns ``(ids, logprobs, kept, status)``.
 * ``dsv41_rocm::selected_log_probs`` — the fused log-prob head; returns
-  ``(logprob, entropy, ratio)`` with an empty ``ratio`` when no behaviour log-probs are given.
+  ``(logprob, entropy, ratio, lse)`` with an empty ``ratio`` when no behaviour log-probs are
+  given.  Differentiable in ``hidden`` and ``weight`` through ``register_autograd`` (the
+  reference registers its Triton ops' backward the same way, moe/kernels.py:283-307);
+  ``ratio`` and ``lse`` carry no gradient.
 
 The ops only register a CUDA (HIP) kernel: called on CPU tensors they raise, as the library
 has no CPU path.  Status bits are returned, not raised, so the ops stay traceable; the
@@ -64,12 +67,12 @@ def selected_log_probs_op(
     temperature: float,
     behavior: Optional[torch.Tensor],
     is_cap: float,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    lp, ent, ratio = _logprob.selected_log_probs(hidden, weight, targets, temperature,
-                                                 behavior=behavior, is_cap=is_cap, check=False)
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    hidden, weight, targets = _logprob._prepare(hidden, weight, targets, temperature)
+    lp, ent, ratio, lse, _ = _logprob._forward(hidden, weight, targets, temperature, behavior, is_cap)
     if ratio is None:
         ratio = lp.new_empty(0)
-    return lp, ent, ratio
+    return lp, ent, ratio, lse
 
 
 @selected_log_probs_op.register_fake
@@ -79,7 +82,32 @@ def _selected_log_probs_fake(hidden, weight, targets, temperature, behavior, is_
     lp = torch.empty(n, dtype=torch.float32, device=dev)
     ent = torch.empty(n, dtype=torch.float32, device=dev)
     ratio = torch.empty(n if behavior is not None else 0, dtype=torch.float32, device=dev)
-    return lp, ent, ratio
+    lse = torch.empty(n, dtype=torch.float32, device=dev)
+    return lp, ent, ratio, lse
+
+
+def _selected_log_probs_setup(ctx, inputs, output):
+    hidden, weight, targets, temperature, _, _ = inputs
+    _, ent, _, lse = output
+    ctx.temperature = temperature
+    ctx.hidden_dtype, ctx.weight_dtype = hidden.dtype, weight.dtype
+    ctx.save_for_backward(hidden, weight, targets, lse, ent)
+
+
+def _selected_log_probs_backward(ctx, g_lp, g_ent, g_ratio, g_lse):
+    hidden, weight, targets, lse, ent = ctx.saved_tensors
+    h, w, t = _logprob._prepare(hidden, weight, targets, ctx.temperature)
+    dx, dw = _logprob.selected_log_probs_backward(h, w, t, ctx.temperature, lse, ent, g_lp, g_ent,
+                                                  need_hidden=ctx.needs_input_grad[0],
+                                                  need_weight=ctx.needs_input_grad[1])
+    if dx is not None:
+        dx = dx.to(ctx.hidden_dtype)
+    if dw is not None:
+        dw = dw.to(ctx.weight_dtype)
+    return dx, dw, None, None, None, None
+
+
+selected_log_probs_op.register_autograd(_selected_log_probs_backward, setup_context=_selected_log_probs_setup)
 
 
 __all__ = ["sample_rows", "selected_log_probs_op"]
