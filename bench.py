@@ -54,6 +54,7 @@ def parse():
                     help="sampler config; 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
     ap.add_argument("--logprob-steps", type=int, default=5)
+    ap.add_argument("--no-backward", action="store_true", help="skip the log-prob backward timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="time a plain device copy of this many bytes (PMC calibration) and exit")
@@ -213,11 +214,12 @@ def main():
         line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
         print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
-        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, not args.no_cpu_baseline, torch)
+        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, not args.no_cpu_baseline, torch,
+                                        backward=not args.no_backward)
     print(json.dumps(line), flush=True)
 
 
-def bench_logprob(name, steps, warmup, cpu_baseline, torch):
+def bench_logprob(name, steps, warmup, cpu_baseline, torch, backward=False):
     """Fused selected-token log-prob over one batch of config C or D (D adds the ratio)."""
     from dsv41_rocm import _lib, selected_log_probs, workloads
 
@@ -271,9 +273,41 @@ def bench_logprob(name, steps, warmup, cpu_baseline, torch):
                      "frac": achieved / BF16_PEAK_TFLOPS, "traffic": MEASURED_TRAFFIC.get(f"logprob_{name}"),
                      "flops_per_token": 2.0 * h * v},
     }
+    if backward:
+        out["backward"] = bench_logprob_backward(x, w, t, lp, ent, steps, torch)
     if cpu_baseline:
         out["cpu_baseline"] = cpu_logprob_baseline(x, w, t, torch)
     return out
+
+
+def bench_logprob_backward(x, w, t, lp, ent, steps, torch):
+    """Backward of the fused log-prob for dL/dlogprob = 1 per token: the logit-gradient
+    kernel (logits recomputed on MFMA, bf16 gradient written once) and the whole backward
+    with the two GEMMs (hipBLASLt through torch) that produce dL/dx and dL/dw."""
+    from dsv41_rocm import logprob as lpmod
+
+    n, h = x.shape
+    v = w.shape[0]
+    hx, hw, ht = lpmod._prepare(x, w, t, 1.0)
+    _, ent_, _, lse, _ = lpmod._forward(hx, hw, ht, 1.0, None, 2.0)
+    glp = torch.ones(n, dtype=torch.float32, device=x.device)
+    kern = events_time(lambda: lpmod.logits_grad(hx, hw, ht, 1.0, lse, ent_, glp, None), steps, 1, torch)
+    full = events_time(lambda: lpmod.selected_log_probs_backward(hx, hw, ht, 1.0, lse, ent_, glp, None),
+                       steps, 1, torch)
+    flops = 2.0 * n * h * v
+    return {
+        "ms_per_step": full,
+        "value": n / (full * 1e-3),
+        "unit": "tok/s",
+        "flops_per_token": 3 * 2.0 * h * v,
+        "tflops": 3 * flops / (full * 1e-3) / 1e12,
+        "grad_kernel": {"ms": kern, "roofline": {"bound": "mfma", "achieved": flops / (kern * 1e-3) / 1e12,
+                                                 "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                                 "frac": flops / (kern * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                                                 "flops_per_token": 2.0 * h * v,
+                                                 "bf16_out_bytes": 2 * n * v}},
+        "gemms": "dL/dx = G @ w and dL/dw = G^T @ x, torch.mm (hipBLASLt)",
+    }
 
 
 def cpu_logprob_baseline(x, w, t, torch):

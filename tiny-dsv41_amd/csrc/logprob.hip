@@ -52,8 +52,6 @@ constexpr int KS = BK / 16;                  // MFMA k-steps per stage
 constexpr int ROWB = BK * 2;                 // bytes per LDS row: one 128-byte cache line
 constexpr int STAGE_BYTES = (BV + BT) * ROWB;  // 64 KiB
 constexpr int LDS_BYTES = 2 * STAGE_BYTES;   // two stage buffers
-constexpr int GROW = BV * 2 + 16;            // bytes per token row of the backward's staged bf16 tile
-constexpr int GRAD_LDS = BT * GROW > LDS_BYTES ? BT * GROW : LDS_BYTES;
 constexpr int ROWS_PER_LOAD = 1024 / ROWB;   // rows one wave-wide 16-byte LDS load fills
 constexpr int A_LOADS = BV / NWAVES / ROWS_PER_LOAD;  // per wave per stage
 constexpr int B_LOADS = BT / NWAVES / ROWS_PER_LOAD;
@@ -198,29 +196,26 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Backward epilogue of one 256 x 256 block: dL/dz per element from the recomputed logit,
-// scaled by 1/T and rounded to bf16, staged transposed in LDS (token rows of GROW bytes)
-// and written out as 16-byte pieces of output rows.
-__device__ __forceinline__ void grad_block(const Params& p, unsigned char* lds, const floatx16 (&acc)[WV][WT],
-                                           int t0, int vb, int wv, int wt, int lane) {
-  const int tid = threadIdx.x, r32 = lane & 31, half = lane >> 5;
-  __builtin_amdgcn_s_waitcnt(0);  // every load of this wave landed (also the zero loads past the end)
-  __syncthreads();                // and every wave's: the stage buffers are free
+// Backward epilogue of one vocabulary block: dL/dz per element from the recomputed logit,
+// scaled by 1/T and rounded to bf16, written straight from the accumulators (each lane
+// stores its four consecutive vocabulary rows of a token as 8 bytes; the lines of an
+// output row fill up in L2 across the wave's stores).
+__device__ __forceinline__ void grad_block(const Params& p, const floatx16 (&acc)[WV][WT], int t0, int vb, int wv,
+                                           int wt, int lane) {
+  const int r32 = lane & 31, half = lane >> 5;
+  const int cols = min(BV, p.V - vb * BV);
 #pragma unroll
   for (int j = 0; j < WT; ++j) {
-    const int nl = wt * (WT * 32) + j * 32 + r32;
-    const int n = t0 + nl;
-    float lse = 0.0f, glp = 0.0f, gent = 0.0f, cent = 0.0f;
-    int tl = -1;  // target row within this block, if there
-    if (n < p.N) {
-      lse = p.lse[n];
-      glp = p.glp ? p.glp[n] : 0.0f;
-      gent = p.gent ? p.gent[n] : 0.0f;
-      cent = p.gent ? lse - p.ent[n] : 0.0f;  // lse - entropy = E[z]
-      const int64_t t = p.targets[n] - p.vbeg - (int64_t)vb * BV;
-      tl = (t >= 0 && t < BV) ? (int)t : -1;
-    }
+    const int n = t0 + wt * (WT * 32) + j * 32 + r32;
+    if (n >= p.N) continue;
+    const float lse = p.lse[n];
+    const float glp = p.glp ? p.glp[n] : 0.0f;
+    const float gent = p.gent ? p.gent[n] : 0.0f;
+    const float cent = p.gent ? lse - p.ent[n] : 0.0f;  // lse - entropy = E[z]
+    const int64_t tt = p.targets[n] - p.vbeg - (int64_t)vb * BV;
+    const int tl = (tt >= 0 && tt < BV) ? (int)tt : -1;  // target row within this block, if there
     const float mb = lse * LOG2E, c1 = p.invT * LOG2E;
+    uint16_t* row = p.out + (int64_t)n * p.os + (int64_t)vb * BV;
 #pragma unroll
     for (int i = 0; i < WV; ++i)
 #pragma unroll
@@ -239,28 +234,20 @@ __device__ __forceinline__ void grad_block(const Params& p, unsigned char* lds, 
         uint2 w2;
         w2.x = pack_bf16(gv[0], gv[1]);
         w2.y = pack_bf16(gv[2], gv[3]);
-        *reinterpret_cast<uint2*>(lds + nl * GROW + v0 * 2) = w2;
+        if (v0 + 4 <= cols) {
+          *reinterpret_cast<uint2*>(row + v0) = w2;
+        } else {  // the vocabulary range ends inside these four rows
+          if (v0 < cols) row[v0] = (uint16_t)w2.x;
+          if (v0 + 1 < cols) row[v0 + 1] = (uint16_t)(w2.x >> 16);
+          if (v0 + 2 < cols) row[v0 + 2] = (uint16_t)w2.y;
+        }
       }
-  }
-  __syncthreads();
-  const int rows = min(BT, p.N - t0), cols = min(BV, p.V - vb * BV);
-  for (int idx = tid; idx < BT * (BV / 8); idx += NT) {
-    const int nl = idx / (BV / 8), c0 = (idx % (BV / 8)) * 8;
-    if (nl >= rows || c0 >= cols) continue;
-    const uint4 val = *reinterpret_cast<const uint4*>(lds + nl * GROW + c0 * 2);
-    uint16_t* dst = p.out + (int64_t)(t0 + nl) * p.os + (int64_t)vb * BV + c0;
-    if (c0 + 8 <= cols) {
-      *reinterpret_cast<uint4*>(dst) = val;
-    } else {
-      const uint32_t wds[4] = {val.x, val.y, val.z, val.w};
-      for (int e = 0; e < cols - c0; ++e) dst[e] = (uint16_t)(wds[e >> 1] >> ((e & 1) * 16));
-    }
   }
 }
 
 template <bool GRAD>
 __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void fused_kernel(Params p) {
-  __shared__ __align__(16) unsigned char lds[GRAD ? GRAD_LDS : LDS_BYTES];
+  __shared__ __align__(16) unsigned char lds[LDS_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wv = wid % WAVES_V, wt = wid / WAVES_V;
@@ -396,7 +383,7 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     // end of a vocabulary block: lane holds rows 8*(r/4) + 4*(lane/32) + r%4 of each
     // 32-row block, at offsets from rbase that are compile-time constants
     if constexpr (GRAD) {
-      grad_block(p, lds, acc, t0, vb, wv, wt, lane);  // the backward's grid has one block per workgroup
+      grad_block(p, acc, t0, vb, wv, wt, lane);
       continue;
     }
     const int rbase = vb * BV + wv * (WV * 32) + 4 * half;
@@ -518,6 +505,13 @@ struct Plan {
   size_t workspace;
 };
 
+// One workgroup per CU: split the vocabulary so token blocks x splits fills the machine,
+// at least one vocabulary block per split (ranges are spread evenly).
+int split_count(int n_tb, int n_vb) {
+  const int want = n_tb > 0 ? std::max(1, CU_COUNT / n_tb) : 1;
+  return std::max(1, std::min(want, n_vb));
+}
+
 // XCD super tiles of 32 workgroups (token blocks x splits) when the grid tiles.
 void xcd_groups(Plan* pl) {
   pl->group_t = 0;
@@ -554,16 +548,14 @@ int plan(const dsv41_logprob_desc* d, Plan* pl) {
     return fail(DSV41_E_INVALID, "x, w, targets and out_logprob are required");
   pl->n_vb = (d->vocab + BV - 1) / BV;
   pl->n_tb = (d->n_tokens + BT - 1) / BT;
-  // one workgroup per CU: split the vocabulary so token blocks x splits fills the
-  // machine, at least one vocabulary block per split (ranges are spread evenly)
-  const int want = pl->n_tb > 0 ? std::max(1, CU_COUNT / pl->n_tb) : 1;
-  pl->splits = std::max(1, std::min(want, pl->n_vb));
+  pl->splits = split_count(pl->n_tb, pl->n_vb);
   xcd_groups(pl);
   pl->workspace = (size_t)pl->splits * (size_t)d->n_tokens * sizeof(float4);
   return DSV41_OK;
 }
 
-// Backward: one workgroup per 256 x 256 block of the vocabulary range x tokens.
+// Backward: the forward's grid over the vocabulary range; each workgroup writes the
+// logit gradient of every block it sweeps.
 int plan_grad(const dsv41_logprob_grad_desc* d, Plan* pl) {
   if (!d) return fail(DSV41_E_INVALID, "log-prob gradient descriptor is NULL");
   if (d->struct_size != sizeof(dsv41_logprob_grad_desc))
@@ -588,7 +580,7 @@ int plan_grad(const dsv41_logprob_grad_desc* d, Plan* pl) {
   if (d->grad_entropy && !d->entropy) return fail(DSV41_E_INVALID, "an entropy gradient requires the entropies");
   pl->n_vb = (d->vocab_end - d->vocab_begin + BV - 1) / BV;
   pl->n_tb = (d->n_tokens + BT - 1) / BT;
-  pl->splits = pl->n_vb;
+  pl->splits = split_count(pl->n_tb, pl->n_vb);
   xcd_groups(pl);
   pl->workspace = 0;
   return DSV41_OK;
