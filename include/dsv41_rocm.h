@@ -18,6 +18,8 @@
  *   dsv41_logprob_run  <- dsv41_train/models/dsv4/model.py:679-684 (_token_log_probs),
  *                         dsv41_train/rl/native_lora.py:80-82 (_score_targets),
  *                         plus the Token-TIS weight of dsv41_train/rl/algorithm.py:293-299.
+ *   dsv41_token_tis_run <- dsv41_train/rl/algorithm.py:249-346 (decoupled_token_tis_loss)
+ *                         with the metric pooling of dsv41_train/rl/distributed_grpo.py:197-222.
  *   dsv41_logprob_grad_run <- the autograd backward of that expression as the learner
  *                         differentiates it (dsv41_train/rl/distributed_grpo.py:352-375 over
  *                         native_lora.py:120-122 / model.py:735-738): the gradient with
@@ -156,11 +158,84 @@ typedef struct dsv41_logprob_grad_desc {
   int64_t out_row_stride;   /* in elements, >= vocab_end - vocab_begin, multiple of 8 */
 } dsv41_logprob_grad_desc;
 
+/*
+ * Decoupled Token-TIS loss over a packed batch of responses (response r owns tokens
+ * [offsets[r], offsets[r+1]) of the per-token vectors; each response nonempty):
+ *   delta = f32(native_old - behavior);  raw = exp(f64(delta));  w = f32(min(raw, is_cap))
+ *   ratio = exp(f32(current - native_old))
+ *   s = min(ratio * A_r, clamp(ratio, f32(1 - clip_eps), f32(1 + clip_eps)) * A_r)
+ *   out_loss = mean_r( -mean_{i in r}(w_i * s_i) )                           (fp32)
+ *   out_grad[i] = d out_loss / d current[i]  (torch's minimum / clamp gradient rules)
+ *   out_metrics[DSV41_TIS_M_*]: the diagnostics of the reference's metric dict (fp64),
+ *   pooled over all responses as aggregate_token_tis_metrics pools per-response rows.
+ *   out_status[r]: DSV41_TIS_* bits of the reference's per-response checks.
+ */
+typedef struct dsv41_token_tis_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_token_tis_desc) */
+  int32_t n_responses;  /* R > 0 */
+  int64_t n_tokens;          /* length of the per-token vectors */
+  const int64_t* offsets;    /* [R + 1], nondecreasing, in [0, n_tokens] */
+  const float* current;      /* [tokens] learner log-probs */
+  const float* native_old;   /* [tokens] */
+  const float* behavior;     /* [tokens] */
+  const float* advantages;   /* [R] */
+  double clip_eps;           /* finite, in [0, 1) */
+  double is_cap;             /* finite, > 0 */
+  float* out_loss;           /* [1] or NULL */
+  float* out_grad;           /* [tokens] or NULL */
+  double* out_metrics;       /* [DSV41_TIS_METRICS] or NULL */
+  int32_t* out_status;       /* [R] */
+} dsv41_token_tis_desc;
+
+/* out_status bits of dsv41_token_tis_run, in the reference's check order. */
+#define DSV41_TIS_CURRENT_NONFINITE 0x1
+#define DSV41_TIS_CURRENT_POSITIVE 0x2   /* a value > 1e-6 */
+#define DSV41_TIS_OLD_NONFINITE 0x4
+#define DSV41_TIS_OLD_POSITIVE 0x8
+#define DSV41_TIS_BEHAVIOR_NONFINITE 0x10
+#define DSV41_TIS_BEHAVIOR_POSITIVE 0x20
+#define DSV41_TIS_RAW_NONFINITE 0x40
+#define DSV41_TIS_RAW_ZERO 0x80
+#define DSV41_TIS_WEIGHT_NONFINITE 0x100
+#define DSV41_TIS_WEIGHT_ZERO 0x200
+#define DSV41_TIS_RATIO_NONFINITE 0x400
+#define DSV41_TIS_RATIO_ZERO 0x800
+#define DSV41_TIS_EMPTY 0x1000
+#define DSV41_TIS_ADV_NONFINITE 0x2000
+#define DSV41_TIS_BAD_OFFSETS 0x4000     /* offsets outside [0, n_tokens] or decreasing */
+
+/* out_metrics indices (the reference's metric keys, algorithm.py:322-346). */
+#define DSV41_TIS_M_LOSS 0
+#define DSV41_TIS_M_POLICY_LOSS 1
+#define DSV41_TIS_M_RESPONSE_COUNT 2
+#define DSV41_TIS_M_TOKEN_COUNT 3
+#define DSV41_TIS_M_IS_CAP 4
+#define DSV41_TIS_M_WEIGHT_SUM 5
+#define DSV41_TIS_M_WEIGHT_SQUARE_SUM 6
+#define DSV41_TIS_M_WEIGHT_MEAN 7
+#define DSV41_TIS_M_WEIGHT_MIN 8
+#define DSV41_TIS_M_WEIGHT_MAX 9
+#define DSV41_TIS_M_RAW_WEIGHT_SUM 10
+#define DSV41_TIS_M_RAW_WEIGHT_MIN 11
+#define DSV41_TIS_M_RAW_WEIGHT_MAX 12
+#define DSV41_TIS_M_CLIPPED_TOKENS 13
+#define DSV41_TIS_M_CLIPPED_FRACTION 14
+#define DSV41_TIS_M_DROPPED_MASS 15
+#define DSV41_TIS_M_DROPPED_MASS_FRACTION 16
+#define DSV41_TIS_M_ESS 17
+#define DSV41_TIS_M_ESS_FRACTION 18
+#define DSV41_TIS_M_DELTA_MEAN 19
+#define DSV41_TIS_M_DELTA_MAX_ABS 20
+#define DSV41_TIS_M_RATIO_MEAN 21
+#define DSV41_TIS_M_RATIO_CLIP_FRACTION 22
+#define DSV41_TIS_METRICS 23
+
 /* ABI identity. */
 int dsv41_abi_version(void);
 size_t dsv41_sampler_desc_size(void);
 size_t dsv41_logprob_desc_size(void);
 size_t dsv41_logprob_grad_desc_size(void);
+size_t dsv41_token_tis_desc_size(void);
 const char* dsv41_last_error(void);
 
 /* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch. */
@@ -175,6 +250,12 @@ int dsv41_logprob_run(const dsv41_logprob_desc* desc, void* workspace, size_t wo
 
 /* Gradient of the fused log-prob with respect to the logits (no workspace). */
 int dsv41_logprob_grad_run(const dsv41_logprob_grad_desc* desc, void* stream /* hipStream_t */);
+
+/* Token-TIS loss, gradient and metrics: replaces algorithm.py:249-346 for a batch of
+ * responses, pooled as distributed_grpo.py:197-222. */
+size_t dsv41_token_tis_workspace_bytes(const dsv41_token_tis_desc* desc);
+int dsv41_token_tis_run(const dsv41_token_tis_desc* desc, void* workspace, size_t workspace_bytes,
+                        void* stream /* hipStream_t */);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,8 @@ TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 * ``logprob_oracle`` (numpy fp64) restates ``dsv41_train/models/dsv4/model.py:679-684``,
   ``dsv41_train/rl/native_lora.py:80-82`` and the Token-TIS weight of
   ``dsv41_train/rl/algorithm.py:293-299``; ``logprob_grad_oracle`` its backward.
+* ``token_tis_loss_oracle`` (numpy) restates ``decoupled_token_tis_loss``,
+  ``dsv41_train/rl/algorithm.py:249-346``, with its gradient and pooled metrics.
 
 Pinning: tests/test_oracle_sampler.py and tests/test_oracle_logprob.py check every
 function here against closed forms, brute force on tiny inputs, libm, torch and the
@@ -26,6 +28,7 @@ from pathlib import Path
 import numpy as np
 
 from .logprob_oracle import logprob_grad_oracle, logprob_oracle, token_tis_weight  # noqa: F401
+from .tis_oracle import grpo_loss_oracle, token_tis_loss_oracle  # noqa: F401
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle_dsv41.so"

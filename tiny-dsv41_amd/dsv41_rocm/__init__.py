@@ -1,8 +1,9 @@
 """dsv41_rocm — MI355X (gfx950) token sampler and fused selected-token log-prob.
 
-Drop-in for Tiny-DSV41's rollout sampling step (``dsv41_train/rl/rollout.py:144-150``) and
-its selected-token log-prob head (``dsv41_train/models/dsv4/model.py:679-684``,
-``dsv41_train/rl/native_lora.py:80-82``), backed by hand-written HIP kernels in
+Drop-in for Tiny-DSV41's rollout sampling step (``dsv41_train/rl/rollout.py:144-150``), its
+selected-token log-prob head (``dsv41_train/models/dsv4/model.py:679-684``,
+``dsv41_train/rl/native_lora.py:80-82``) with its backward, and the decoupled Token-TIS loss
+(``dsv41_train/rl/algorithm.py:249-346``), backed by hand-written HIP kernels in
 ``libdsv41hip.so`` (C ABI: ``include/dsv41_rocm.h``).
 """
 
@@ -10,6 +11,8 @@ from ._lib import load as load_library  # noqa: F401
 from .logprob import score_targets, selected_log_probs, token_log_probs  # noqa: F401
 from .ops import sample_rows, selected_log_probs_op  # noqa: F401  (registers torch.ops.dsv41_rocm)
 from .sampling import SampleResult, sample, sample_next, validate_temperature  # noqa: F401
+from .tis import decoupled_token_tis_loss  # noqa: F401
 
 __all__ = ["SampleResult", "sample", "sample_next", "validate_temperature", "load_library",
-           "selected_log_probs", "score_targets", "token_log_probs", "sample_rows", "selected_log_probs_op"]
+           "selected_log_probs", "score_targets", "token_log_probs", "sample_rows", "selected_log_probs_op",
+           "decoupled_token_tis_loss"]
