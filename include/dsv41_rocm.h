@@ -95,6 +95,12 @@ typedef struct dsv41_sampler_desc {
   float* out_logprob;          /* [rows] */
   int32_t* out_kept;           /* [rows] or NULL */
   int32_t* out_status;         /* [rows] */
+  /* Exponential-race draw (no truncation only): token = argmax_i p_i / exponentials[r, i]
+   * with p = exp(log_softmax(z)) in fp32, first index on ties: torch.multinomial(p, 1) as
+   * the CPU computes it (exponential_ then argmax(p / E)) when fed the same variates.
+   * NULL: inverse CDF against uniforms. */
+  const float* exponentials;       /* [rows, exponentials_row_stride] or NULL */
+  int64_t exponentials_row_stride; /* in elements, >= vocab */
 } dsv41_sampler_desc;
 
 /*

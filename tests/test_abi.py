@@ -79,6 +79,8 @@ def _sampler_desc(**kw):
     (dict(uniforms=None), _lib.E_INVALID, "uniform"),
     (dict(vocab=(1 << 21) + 1, logits_row_stride=(1 << 21) + 1), _lib.E_UNSUPPORTED, "2^21"),
     (dict(struct_size=8), _lib.E_ABI, "size mismatch"),
+    (dict(exponentials=0x6000, exponentials_row_stride=100, top_k=5), _lib.E_UNSUPPORTED, "exponential race"),
+    (dict(exponentials=0x6000, exponentials_row_stride=99), _lib.E_INVALID, "exponentials row stride"),
 ])
 def test_sampler_rejects_bad_descriptors_before_launch(kw, code, msg):
     lib = _lib.load()

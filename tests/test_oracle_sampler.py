@@ -224,3 +224,21 @@ def test_reference_rollout_toy_model_known_answers():
     seen = {int(oracle.sample(zeros, uniforms=np.array([u], np.float32), temperature=T)[0][0])
             for u in np.linspace(0, 1, 30, endpoint=False)}
     assert seen == {0, 1, 2}  # every vocabulary token is reachable (test_rl_rollout.py:105-110)
+
+
+def test_torch_multinomial_is_an_exponential_race_on_the_cpu():
+    """The library behaviour the exponential-race draw relies on (torch, not the reference):
+    torch.multinomial(p, 1, generator=g) on the CPU equals argmax(p / E) with
+    E = empty_like(p).exponential_(1, generator=g), leaves g in the same state, and filling
+    [rows, V] at once consumes the stream as rows one after another."""
+    for V in (3, 1000, 151936):
+        for seed in range(20 if V < 151936 else 2):
+            p = torch.softmax(3 * torch.randn(V, generator=torch.Generator().manual_seed(100 + seed)), 0)
+            g1, g2 = torch.Generator().manual_seed(seed), torch.Generator().manual_seed(seed)
+            a = int(torch.multinomial(p, 1, generator=g1))
+            b = int(torch.argmax(p / torch.empty_like(p).exponential_(1, generator=g2)))
+            assert a == b and torch.equal(g1.get_state(), g2.get_state())
+    g1, g2 = torch.Generator().manual_seed(9), torch.Generator().manual_seed(9)
+    bulk = torch.empty(4, 5000).exponential_(1, generator=g1)
+    rows = torch.stack([torch.empty(5000).exponential_(1, generator=g2) for _ in range(4)])
+    assert torch.equal(bulk, rows) and torch.equal(g1.get_state(), g2.get_state())

@@ -71,6 +71,8 @@ struct Params {
   int32_t* out_kept;
   int32_t* out_status;
   float* zbuf;
+  const float* exps;  // exponential-race draw: [rows, estride] Exp(1) variates, or NULL
+  int64_t estride;
   double log_min_p;
   float T, rT, rp, pres, freq, top_p, min_p, lmin_f;
   int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words, cap;
@@ -857,6 +859,81 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   __syncthreads();
   for (int s = tid; s < U; s += NT) atomicAdd(&cs[h.tok[s] / (64 * G)], exp2f((penz[s] - M) * LOG2E));
   __syncthreads();
+
+  if (p.exps && !p.greedy) {
+    // Exponential race: the token is argmax_i p_i / E_i with p_i = exp(log_softmax(z)_i),
+    // each step in fp32 as torch forms it (log_softmax = z - (max + log(sum)), exp,
+    // division), first index on ties.  This is torch.multinomial(p, 1) on the CPU fed the
+    // same E (its draw is exponential_ followed by argmax(p / E)); only the order of the
+    // sum differs, which moves every p by the same factor and can reorder only ratios
+    // within an ulp of each other.
+    __syncthreads();
+    float csum = 0.0f;
+    for (int c = tid; c < NC; c += NT) csum += cs[c];
+    const double S = (double)block_sum_d<NT>((double)csum, m);
+    const float lsum = M + logf((float)S);
+    const float* erow = p.exps + (int64_t)row * p.estride;
+    const __amdgpu_buffer_rsrc_t re = row_rsrc(erow, (uint32_t)p.V * 4u);
+    float best = -1.0f;
+    int bidx = 0x7FFFFFFF;
+    auto offer = [&](float z, float ev, int idx) {
+      const float pr = expf(z - lsum);
+      const float r = pr / ev;
+      if (r > best || (r == best && idx < bidx)) {
+        best = r;
+        bidx = idx;
+      }
+    };
+    const int nt = (p.V + TILE - 1) / TILE;
+    for (int t = 0; t < nt; ++t) {
+      const int base = t * TILE + tid * G;
+      Raw<TIn, G> r;
+      load_group<TIn, G, VEC>(r, rs, base);
+      Raw<float, G> er;
+      load_group<float, G, false>(er, re, base);
+      float x[G], z[G];
+      unpack(r, x);
+      int dummy = 0;
+      make_z<G, true>(x, base, p, h.bitmap, z, dummy);  // history tokens and the tail read -inf
+#pragma unroll
+      for (int j = 0; j < G; ++j)
+        if (base + j < p.V && z[j] > NEG_INF) offer(z[j], __uint_as_float(er.w[j]), base + j);
+    }
+    for (int s = tid; s < U; s += NT) offer(penz[s], erow[h.tok[s]], (int)h.tok[s]);
+    // fixed-order argmax: waves by shuffles, then waves in turn
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o);
+      const int oi = __shfl_xor(bidx, o);
+      if (ob > best || (ob == best && oi < bidx)) {
+        best = ob;
+        bidx = oi;
+      }
+    }
+    if (lane == 0) {
+      m->rf[wid] = best;
+      m->ri[wid] = bidx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float b = m->rf[0];
+      int bi = m->ri[0];
+      for (int w = 1; w < NW; ++w)
+        if (m->rf[w] > b || (m->rf[w] == b && m->ri[w] < bi)) {
+          b = m->rf[w];
+          bi = m->ri[w];
+        }
+      const int64_t tok = bi == 0x7FFFFFFF ? 0 : bi;
+      float ztok = M;
+      if (bi != 0x7FFFFFFF) {
+        const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
+        ztok = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
+      }
+      const float lp = (float)(((double)ztok - (double)M) - log(S));
+      write_result(p, row, m, tok, lp, p.V);
+    }
+    return;
+  }
 
   // total mass and the chunk holding the draw (wave 0, fp64)
   const float u = row_uniform(p, row, m);
@@ -1646,6 +1723,10 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
   pl->vec = ((uintptr_t)d->logits % 16 == 0) && ((d->logits_row_stride * pl->esize) % 16 == 0);
   const int V = d->vocab;
   const bool truncating = d->min_p > 0.0f || (d->top_k > 0 && d->top_k < V) || d->top_p < 1.0f;
+  if (d->exponentials && truncating)
+    return fail(DSV41_E_UNSUPPORTED, "exponential race draws need the full-vocabulary distribution (no top-k, top-p or min-p)");
+  if (d->exponentials && d->exponentials_row_stride < d->vocab)
+    return fail(DSV41_E_INVALID, "exponentials row stride must be >= vocab");
   if (!truncating) pl->mode = MODE_FULL;
   else if (d->top_k > 0 && d->top_k < V && d->top_k <= KCAP) pl->mode = MODE_TOPK;
   else pl->mode = MODE_GENERIC;
@@ -1700,6 +1781,8 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   p.out_kept = d->out_kept;
   p.out_status = d->out_status;
   p.zbuf = static_cast<float*>(workspace);
+  p.exps = d->exponentials;
+  p.estride = d->exponentials_row_stride;
   p.log_min_p = d->min_p > 0.0f ? std::log((double)d->min_p) : -INFINITY;
   {
     // log(min_p) as a float rounded toward -inf, for the conservative in-stream bound

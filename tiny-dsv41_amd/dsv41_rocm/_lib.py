@@ -58,6 +58,8 @@ class SamplerDesc(ctypes.Structure):
         ("out_logprob", ctypes.c_void_p),
         ("out_kept", ctypes.c_void_p),
         ("out_status", ctypes.c_void_p),
+        ("exponentials", ctypes.c_void_p),
+        ("exponentials_row_stride", ctypes.c_int64),
     ]
 
 

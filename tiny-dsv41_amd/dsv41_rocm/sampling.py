@@ -76,6 +76,7 @@ def sample(
     min_p: float = 0.0,
     greedy: bool = False,
     check: bool = True,
+    exponentials: Optional[torch.Tensor] = None,
 ) -> SampleResult:
     """Sample one token per row of ``logits[rows, vocab]`` (fp32 or bf16, on the GPU).
 
@@ -84,6 +85,12 @@ def sample(
     drive the draw; when omitted they are drawn with ``torch.rand(rows, generator=generator)``
     on the CPU.  With ``check`` the call synchronises and raises the reference's
     ``ValueError`` for non-finite rows, out-of-vocabulary history or bad uniforms.
+
+    ``exponentials`` (fp32 ``[rows, vocab]`` of Exp(1) variates) switches the draw to the
+    exponential race ``argmax(p / E)``, which is what ``torch.multinomial(p, 1)`` computes on
+    the CPU; fed the variates of ``torch.empty(V).exponential_(1, generator=g)`` it returns
+    the reference's token (rollout.py:147-148) and leaves ``g`` where the reference leaves it.
+    Only without top-k / top-p / min-p.
     """
     validate_temperature(temperature)
     if not isinstance(logits, torch.Tensor) or logits.ndim != 2 or 0 in logits.shape:
@@ -98,6 +105,13 @@ def sample(
         raise ValueError("top_k must be a nonnegative integer")
     rows, vocab = logits.shape
     device = logits.device
+    if exponentials is not None and not greedy:
+        exponentials = exponentials.to(device=device, dtype=torch.float32)
+        if exponentials.ndim != 2 or exponentials.shape != logits.shape:
+            raise ValueError("exponentials must have the shape of logits")
+        if exponentials.stride(1) != 1:
+            exponentials = exponentials.contiguous()
+        uniforms = torch.zeros(rows, dtype=torch.float32, device=device) if uniforms is None else uniforms
     if not greedy:
         if uniforms is None:
             if generator is not None and generator.device.type != "cpu":
@@ -145,6 +159,9 @@ def sample(
     desc.out_logprob = lps.data_ptr()
     desc.out_kept = kept.data_ptr()
     desc.out_status = status.data_ptr()
+    if exponentials is not None and not greedy:
+        desc.exponentials = exponentials.data_ptr()
+        desc.exponentials_row_stride = exponentials.stride(0)
     lib = _lib.load()
     ws_bytes = lib.dsv41_sampler_workspace_bytes(_lib.ctypes.byref(desc))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
@@ -159,14 +176,27 @@ def sample(
 
 
 def sample_next(logits: torch.Tensor, temperature: float,
-                generator: Optional[torch.Generator] = None, **knobs) -> tuple[int, float]:
+                generator: Optional[torch.Generator] = None, draw: str = "inverse_cdf",
+                **knobs) -> tuple[int, float]:
     """Drop-in for rollout.py:144-150 on one ``[V]`` (or ``[1, V]``) logits row.
 
     Returns ``(token, behavior_log_prob)`` like the reference's ``token`` /
-    ``float(log_probs[token])``; the uniform comes from ``torch.rand(1, generator=generator)``.
+    ``float(log_probs[token])``.  ``draw="inverse_cdf"`` takes one uniform from
+    ``torch.rand(1, generator=generator)``; ``draw="exponential_race"`` takes the V variates of
+    ``torch.empty(V).exponential_(1, generator=generator)``, exactly what the reference's
+    ``torch.multinomial(probabilities, 1, generator=generator)`` consumes, and so draws the
+    reference's token and leaves the generator in the reference's state.
     """
     row = logits.reshape(1, -1) if logits.ndim == 1 else logits
     if row.ndim != 2 or row.shape[0] != 1:
         raise ValueError("model next_token_logits must return [1, vocabulary_size]")
-    result = sample(row, temperature=temperature, generator=generator, **knobs)
+    if draw == "exponential_race":
+        if generator is not None and generator.device.type != "cpu":
+            raise ValueError("generation requires a CPU torch.Generator")
+        e = torch.empty(1, row.shape[1], dtype=torch.float32).exponential_(1, generator=generator)
+        result = sample(row, temperature=temperature, exponentials=e, **knobs)
+    elif draw == "inverse_cdf":
+        result = sample(row, temperature=temperature, generator=generator, **knobs)
+    else:
+        raise ValueError("draw must be 'inverse_cdf' or 'exponential_race'")
     return int(result.ids.item()), float(result.logprobs.item())
