@@ -33,11 +33,12 @@ BF16_PEAK_TFLOPS = 2500.0
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by
 # the same counters on a plain 1 GiB copy (FETCH x 2.0, WRITE x 1.0); the commands and raw
-# counts are in profiles/sampler_topk_E.md and profiles/logprob_fused_D.md.  Workloads
-# without an entry report null.
+# counts are in profiles/sampler_topk_E.md, profiles/logprob_fused_D.md and
+# profiles/logprob_backward_D.md.  Workloads without an entry report null.
 MEASURED_TRAFFIC = {
-    "sampler_E": 2_649_526_272 + 575_480,
-    "logprob_D": 74_377_687_040 + 2_097_152,
+    "sampler_E": 2_657_643_808 + 600_544,
+    "logprob_D": 45_660_437_888 + 1_048_576,
+    "logprob_grad_D": 45_297_095_573 + 4_384_320_091,
 }
 
 
@@ -295,6 +296,7 @@ def bench_logprob_backward(x, w, t, lp, ent, steps, torch):
     full = events_time(lambda: lpmod.selected_log_probs_backward(hx, hw, ht, 1.0, lse, ent_, glp, None),
                        steps, 1, torch)
     flops = 2.0 * n * h * v
+    name = "D" if (n, h, v) == (16384, 7168, 129280) else "C" if (n, h, v) == (8192, 2048, 151936) else "?"
     return {
         "ms_per_step": full,
         "value": n / (full * 1e-3),
@@ -305,7 +307,8 @@ def bench_logprob_backward(x, w, t, lp, ent, steps, torch):
                                                  "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                                  "frac": flops / (kern * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                                                  "flops_per_token": 2.0 * h * v,
-                                                 "bf16_out_bytes": 2 * n * v}},
+                                                 "bf16_out_bytes": 2 * n * v,
+                                                 "traffic": MEASURED_TRAFFIC.get(f"logprob_grad_{name}")}},
         "gemms": "dL/dx = G @ w and dL/dw = G^T @ x, torch.mm (hipBLASLt)",
     }
 
