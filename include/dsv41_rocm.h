@@ -18,6 +18,7 @@
  *   dsv41_logprob_run  <- dsv41_train/models/dsv4/model.py:679-684 (_token_log_probs),
  *                         dsv41_train/rl/native_lora.py:80-82 (_score_targets),
  *                         plus the Token-TIS weight of dsv41_train/rl/algorithm.py:293-299.
+ *   dsv41_grpo_run     <- dsv41_train/rl/algorithm.py:169-246 (grpo_loss).
  *   dsv41_token_tis_run <- dsv41_train/rl/algorithm.py:249-346 (decoupled_token_tis_loss)
  *                         with the metric pooling of dsv41_train/rl/distributed_grpo.py:197-222.
  *   dsv41_logprob_grad_run <- the autograd backward of that expression as the learner
@@ -236,12 +237,57 @@ typedef struct dsv41_token_tis_desc {
 #define DSV41_TIS_M_RATIO_CLIP_FRACTION 22
 #define DSV41_TIS_METRICS 23
 
+/*
+ * GRPO loss over a packed batch of responses (same packing as dsv41_token_tis_desc):
+ *   ratio = exp(f32(current - behavior));  s = min(ratio A, clamp(ratio, f32(1-eps), f32(1+eps)) A)
+ *   k3 = ratio * (expm1(reference - current) - (reference - current))   (kl_beta > 0)
+ *   out_loss = mean_r(-mean_i s) + kl_beta * mean_r(mean_i k3)          (fp32)
+ *   out_grad[i] = d out_loss / d current[i]
+ *   out_metrics[DSV41_GRPO_M_*]: loss, policy_loss, kl, clip_fraction, importance_ratio,
+ *   approx_kl as the reference's dict (means over responses of per-response means).
+ */
+typedef struct dsv41_grpo_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_grpo_desc) */
+  int32_t n_responses;  /* R > 0 */
+  int64_t n_tokens;
+  const int64_t* offsets;   /* [R + 1], nondecreasing, in [0, n_tokens] */
+  const float* current;     /* [tokens] */
+  const float* behavior;    /* [tokens] */
+  const float* reference;   /* [tokens]; required when kl_beta > 0 */
+  const float* advantages;  /* [R] */
+  double clip_eps;          /* finite, in [0, 1) */
+  double kl_beta;           /* finite, >= 0 */
+  float* out_loss;          /* [1] or NULL */
+  float* out_grad;          /* [tokens] or NULL */
+  double* out_metrics;      /* [DSV41_GRPO_METRICS] or NULL */
+  int32_t* out_status;      /* [R] */
+} dsv41_grpo_desc;
+
+/* out_status bits of dsv41_grpo_run, in the reference's check order. */
+#define DSV41_GRPO_CURRENT_NONFINITE 0x1
+#define DSV41_GRPO_BEHAVIOR_NONFINITE 0x2
+#define DSV41_GRPO_RATIO_NONFINITE 0x4
+#define DSV41_GRPO_REFERENCE_NONFINITE 0x8
+#define DSV41_GRPO_K3_NONFINITE 0x10
+#define DSV41_GRPO_EMPTY 0x20
+#define DSV41_GRPO_ADV_NONFINITE 0x40
+#define DSV41_GRPO_BAD_OFFSETS 0x80
+
+#define DSV41_GRPO_M_LOSS 0
+#define DSV41_GRPO_M_POLICY_LOSS 1
+#define DSV41_GRPO_M_KL 2
+#define DSV41_GRPO_M_CLIP_FRACTION 3
+#define DSV41_GRPO_M_IMPORTANCE_RATIO 4
+#define DSV41_GRPO_M_APPROX_KL 5
+#define DSV41_GRPO_METRICS 6
+
 /* ABI identity. */
 int dsv41_abi_version(void);
 size_t dsv41_sampler_desc_size(void);
 size_t dsv41_logprob_desc_size(void);
 size_t dsv41_logprob_grad_desc_size(void);
 size_t dsv41_token_tis_desc_size(void);
+size_t dsv41_grpo_desc_size(void);
 const char* dsv41_last_error(void);
 
 /* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch. */
@@ -262,6 +308,11 @@ int dsv41_logprob_grad_run(const dsv41_logprob_grad_desc* desc, void* stream /* 
 size_t dsv41_token_tis_workspace_bytes(const dsv41_token_tis_desc* desc);
 int dsv41_token_tis_run(const dsv41_token_tis_desc* desc, void* workspace, size_t workspace_bytes,
                         void* stream /* hipStream_t */);
+
+/* GRPO loss, gradient and metrics: replaces algorithm.py:169-246 for a batch of responses. */
+size_t dsv41_grpo_workspace_bytes(const dsv41_grpo_desc* desc);
+int dsv41_grpo_run(const dsv41_grpo_desc* desc, void* workspace, size_t workspace_bytes,
+                   void* stream /* hipStream_t */);
 
 #ifdef __cplusplus
 }

@@ -77,15 +77,46 @@ def token_tis_loss_oracle(current, old, behavior, advantages, clip_eps=0.2, is_c
     return loss, grads, dict(zip(METRIC_KEYS, values))
 
 
-def grpo_loss_oracle(current, behavior, advantages, clip_eps=0.2):
-    """grpo_loss without KL (algorithm.py:169-246): mean over responses of the per-response
-    mean of -min(r A, clamp(r) A), r = exp(current - behavior); fp32."""
+def grpo_loss_oracle(current, behavior, advantages, clip_eps=0.2, reference=None, kl_beta=0.0, full=False):
+    """grpo_loss (algorithm.py:169-246) in fp32 per response: ratio = exp(current - behavior),
+    the clipped surrogate mean, and with kl_beta the mean of ratio * (expm1(d) - d),
+    d = reference - current.  Returns the loss, or with ``full`` (loss, grads, metrics), the
+    gradient written out from torch's minimum / clamp rules and d(k3)/d current =
+    ratio * (current - reference)."""
     f32 = np.float32
+    R = len(current)
     lo, hi = f32(1.0 - clip_eps), f32(1.0 + clip_eps)
-    terms = []
-    for c, b, A in zip(current, behavior, np.asarray(advantages, dtype=f32)):
-        ratio = np.exp((np.asarray(c, f32) - np.asarray(b, f32)).astype(f32)).astype(f32)
-        s = np.minimum((ratio * A).astype(f32), (np.clip(ratio, lo, hi) * A).astype(f32))
-        terms.append(-f32(np.mean(s, dtype=f32)))
-    return f32(np.mean(np.asarray(terms, dtype=f32), dtype=f32))
-
+    beta = f32(kl_beta)
+    pols, kls, clips, ratios, akls, grads = [], [], [], [], [], []
+    for r, (c, b, A) in enumerate(zip(current, behavior, np.asarray(advantages, dtype=f32))):
+        c = np.asarray(c, f32)
+        lr = (c - np.asarray(b, f32)).astype(f32)
+        ratio = np.exp(lr).astype(f32)
+        u = (ratio * A).astype(f32)
+        cl = (np.clip(ratio, lo, hi) * A).astype(f32)
+        s = np.minimum(u, cl)
+        pols.append(-f32(np.mean(s, dtype=f32)))
+        gu = np.where(u < cl, 1.0, np.where(u == cl, 0.5, 0.0)).astype(f32)
+        gc = np.where(cl < u, 1.0, np.where(u == cl, 0.5, 0.0)).astype(f32)
+        inside = ((ratio >= lo) & (ratio <= hi)).astype(f32)
+        g = (-(A * (gu + gc * inside) * ratio)).astype(f32)
+        if kl_beta:
+            ref = np.asarray(reference[r], f32)
+            d = (ref - c).astype(f32)
+            k3 = (ratio * (np.expm1(d).astype(f32) - d)).astype(f32)
+            kls.append(f32(np.mean(k3, dtype=f32)))
+            g = (g + beta * (ratio * (c - ref))).astype(f32)
+        else:
+            kls.append(f32(0.0))
+        grads.append((g / f32(c.size) / f32(R)).astype(f32))
+        clips.append(f32(np.mean((np.abs(ratio - f32(1)) > f32(clip_eps)).astype(f32), dtype=f32)))
+        ratios.append(f32(np.mean(ratio, dtype=f32)))
+        akls.append(f32(np.mean(-lr, dtype=f32)))
+    mean = lambda v: f32(np.mean(np.asarray(v, dtype=f32), dtype=f32))
+    policy, kl = mean(pols), mean(kls)
+    loss = f32(policy + beta * kl)
+    if not full:
+        return loss
+    metrics = {"loss": float(loss), "policy_loss": float(policy), "kl": float(kl), "clip_fraction": float(mean(clips)),
+               "importance_ratio": float(mean(ratios)), "approx_kl": float(mean(akls))}
+    return loss, grads, metrics

@@ -122,3 +122,71 @@ def test_argument_checks():
         decoupled_token_tis_loss([torch.zeros(0, device=DEV)], [[]], [[]], [1.0])
     with pytest.raises(ValueError, match="advantages contains non-finite"):
         decoupled_token_tis_loss(c, [[-1.0] * 3], [[-1.0] * 3], [math.nan])
+
+
+# ------------------------------------------------------------------------------- GRPO
+from dsv41_rocm import grpo_loss  # noqa: E402
+
+
+def test_grpo_known_answers_of_reference_tests():
+    # test_rl_algorithm.py:64-75
+    cur = [torch.tensor([math.log(0.25 * 1.5)], device=DEV, requires_grad=True),
+           torch.tensor([math.log(0.25 * 0.5)], device=DEV, requires_grad=True)]
+    loss, m = grpo_loss(cur, [[math.log(0.25)], [math.log(0.25)]], [1.0, -1.0])
+    assert abs(loss.item() - (-1.2 + 0.8) / 2) < 1e-6 and m["clip_fraction"] == 1.0
+    loss.backward()
+    assert all(c.grad.item() == 0.0 for c in cur)
+    # :77-81
+    loss, _ = grpo_loss([torch.tensor([math.log(0.25 * 1.1)], device=DEV),
+                         torch.tensor([math.log(0.25 * 0.7)] * 3, device=DEV)],
+                        [[math.log(0.25)], [math.log(0.25)] * 3], [1.0, 1.0])
+    assert abs(loss.item() + 0.9) < 1e-6
+    # :83-91
+    cur = [torch.tensor([-1.0], device=DEV, requires_grad=True), torch.tensor([-1.0], device=DEV, requires_grad=True)]
+    loss, _ = grpo_loss(cur, [c.detach().clone() for c in cur], torch.tensor([1.0, -1.0]))
+    loss.backward()
+    assert cur[0].grad.item() < 0 < cur[1].grad.item()
+    # :93-112: the behaviour-weighted k3 value and gradient equal KL(pi || ref) and its gradient
+    theta = torch.tensor([0.3, -0.5], device=DEV, requires_grad=True)
+    log_pi = torch.log_softmax(theta, -1)
+    behavior = torch.tensor([0.7, 0.3], device=DEV)
+    reference = torch.tensor([0.4, 0.6], device=DEV)
+    total = 0
+    for t in range(2):
+        sampled, _ = grpo_loss([log_pi[t:t + 1]], [behavior[t:t + 1].log()], [0.0],
+                               ref_log_probs=[reference[t:t + 1].log()], kl_beta=1.0)
+        total = total + behavior[t] * sampled
+    exact = (log_pi.exp() * (log_pi - reference.log())).sum()
+    torch.testing.assert_close(total, exact)
+    g1 = torch.autograd.grad(total, theta, retain_graph=True)[0]
+    g2 = torch.autograd.grad(exact, theta)[0]
+    torch.testing.assert_close(g1, g2)
+
+
+@pytest.mark.parametrize("lens,eps,beta", [([512] * 32, 0.2, 0.0), ([1, 3, 700, 257, 1024, 5], 0.1, 0.05)])
+def test_grpo_matches_oracle_on_random_batches(lens, eps, beta):
+    print(f"case: GRPO {len(lens)} responses, eps {eps}, kl_beta {beta}", flush=True)
+    current, old, behavior, adv = _batch(lens, 3 * sum(lens), 0.3)
+    reference = [np.minimum(o + np.float32(0.1), 0).astype(np.float32) for o in old]
+    cur = [torch.tensor(c, device=DEV, requires_grad=True) for c in current]
+    loss, m = grpo_loss(cur, behavior, adv, clip_eps=eps,
+                        ref_log_probs=[torch.tensor(r) for r in reference] if beta else None, kl_beta=beta)
+    loss.backward()
+    oloss, ograds, om = oracle.grpo_loss_oracle(current, behavior, adv, eps, reference, beta, full=True)
+    assert abs(loss.item() - float(oloss)) <= 1e-6 * max(1.0, abs(float(oloss)))
+    for c, og in zip(cur, ograds):
+        np.testing.assert_allclose(c.grad.cpu().numpy(), og, rtol=1e-5, atol=1e-9)
+    for k in om:
+        tol = 2.0 / sum(lens) if k == "clip_fraction" else 1e-6 * max(1.0, abs(om[k]))
+        assert abs(m[k] - om[k]) <= tol, (k, m[k], om[k])
+
+
+def test_grpo_errors_raise_reference_messages():
+    with pytest.raises(ValueError, match="response lengths"):
+        grpo_loss([torch.tensor([-1.0, -2.0], device=DEV)], [[-1.0]], [1.0])
+    with pytest.raises(ValueError, match="requires reference"):
+        grpo_loss([torch.tensor([-1.0], device=DEV)], [[-1.0]], [1.0], kl_beta=0.1)
+    with pytest.raises(ValueError, match="importance ratios"):
+        grpo_loss([torch.tensor([-1.0], device=DEV)], [[-1000.0]], [1.0])
+    with pytest.raises(ValueError, match="policy log probabilities contains non-finite"):
+        grpo_loss([torch.tensor([math.nan], device=DEV)], [[-1.0]], [1.0])

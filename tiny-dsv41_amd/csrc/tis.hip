@@ -1,5 +1,5 @@
-// tis.hip — decoupled Token-TIS loss, its gradient and its diagnostics for a packed batch
-// of responses, on gfx950.
+// tis.hip — decoupled Token-TIS loss and GRPO loss, their gradients and their diagnostics
+// for a packed batch of responses, on gfx950.
 //
 // Replaces decoupled_token_tis_loss (dsv41_train/rl/algorithm.py:249-346), which loops over
 // responses in Python with a few dozen small tensor ops and a host sync per metric, and the
@@ -257,6 +257,146 @@ __global__ __launch_bounds__(NT) void pool_kernel(Params p) {
   m[DSV41_TIS_M_RATIO_CLIP_FRACTION] = (double)rclipped / tokens;
 }
 
+// ---------------------------------------------------------------------------- GRPO
+// grpo_loss (dsv41_train/rl/algorithm.py:169-246): per response r with A = advantage,
+//   ratio = exp(f32(current - behavior)),  s = min(ratio A, clamp(ratio, 1 - eps, 1 + eps) A)
+//   k3 = ratio * (expm1(ref - current) - (ref - current))                 (when kl_beta > 0)
+//   loss = mean_r(-mean_i s) + kl_beta * mean_r(mean_i k3)
+// with d k3 / d current = ratio * (current - ref); metrics are means over responses of the
+// per-response means (clip fraction, ratio, -log ratio), all fp32 like the reference's.
+struct GPart {
+  float pol, kl, clipf, ratio, akl;
+};
+
+struct GParams {
+  const int64_t* off;
+  const float* cur;
+  const float* beh;
+  const float* ref;
+  const float* adv;
+  double eps;
+  float lo, hi, epsf, beta;
+  int R;
+  int64_t T;
+  GPart* part;
+  float* grad;
+  int32_t* status;
+  float* loss;
+  double* metrics;
+};
+
+__global__ __launch_bounds__(NT) void grpo_response_kernel(GParams p) {
+  __shared__ float sf[NW];
+  __shared__ int si[NW];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const int64_t b0 = p.off[r], e0 = p.off[r + 1];
+  int st = 0;
+  if (b0 < 0 || e0 > p.T || e0 < b0) st |= DSV41_GRPO_BAD_OFFSETS;
+  const int64_t b = min(max(b0, (int64_t)0), p.T), e = min(max(e0, b), p.T);
+  const int64_t L = e - b;
+  const float A = p.adv[r];
+  if (L <= 0) st |= DSV41_GRPO_EMPTY;
+  if (!isfinite(A)) st |= DSV41_GRPO_ADV_NONFINITE;
+  const float invL = L > 0 ? 1.0f / (float)L : 0.0f, invR = 1.0f / (float)p.R;
+  float pol = 0.0f, kl = 0.0f, clip = 0.0f, rs = 0.0f, akl = 0.0f;
+  for (int64_t i = b + tid; i < e; i += NT) {
+    const float c = p.cur[i], h = p.beh[i];
+    if (!isfinite(c)) st |= DSV41_GRPO_CURRENT_NONFINITE;
+    if (!isfinite(h)) st |= DSV41_GRPO_BEHAVIOR_NONFINITE;
+    const float lr = c - h;
+    const float ratio = expf(lr);
+    if (!isfinite(ratio)) st |= DSV41_GRPO_RATIO_NONFINITE;
+    const float u = ratio * A;
+    const float cl = fminf(fmaxf(ratio, p.lo), p.hi) * A;
+    pol += fminf(u, cl);
+    clip += fabsf(ratio - 1.0f) > p.epsf ? 1.0f : 0.0f;
+    rs += ratio;
+    akl += -lr;
+    float g = 0.0f;
+    if (p.grad) {
+      const float gu = u < cl ? 1.0f : (u == cl ? 0.5f : 0.0f);
+      const float gc = cl < u ? 1.0f : (u == cl ? 0.5f : 0.0f);
+      const float inside = (ratio >= p.lo && ratio <= p.hi) ? 1.0f : 0.0f;
+      g = -(A * (gu + gc * inside) * ratio);  // d(-s)/d current
+    }
+    if (p.ref) {
+      const float rf = p.ref[i];
+      if (!isfinite(rf)) st |= DSV41_GRPO_REFERENCE_NONFINITE;
+      const float delta = rf - c;
+      const float k3 = ratio * (expm1f(delta) - delta);
+      if (!isfinite(k3)) st |= DSV41_GRPO_K3_NONFINITE;
+      kl += k3;
+      g += p.beta * (ratio * (c - rf));
+    }
+    if (p.grad) p.grad[i] = g * invL * invR;
+  }
+  pol = block_reduce(pol, Add(), sf);
+  kl = block_reduce(kl, Add(), sf);
+  clip = block_reduce(clip, Add(), sf);
+  rs = block_reduce(rs, Add(), sf);
+  akl = block_reduce(akl, Add(), sf);
+  st = block_reduce(st, Or(), si);
+  if (tid == 0) {
+    GPart q;
+    q.pol = -(pol * invL);
+    q.kl = kl * invL;
+    q.clipf = clip * invL;
+    q.ratio = rs * invL;
+    q.akl = akl * invL;
+    p.part[r] = q;
+    p.status[r] = st;
+  }
+}
+
+__global__ __launch_bounds__(NT) void grpo_pool_kernel(GParams p) {
+  __shared__ float sf[NW];
+  const int tid = threadIdx.x;
+  float pol = 0.0f, kl = 0.0f, clip = 0.0f, rs = 0.0f, akl = 0.0f;
+  for (int r = tid; r < p.R; r += NT) {
+    const GPart q = p.part[r];
+    pol += q.pol;
+    kl += q.kl;
+    clip += q.clipf;
+    rs += q.ratio;
+    akl += q.akl;
+  }
+  pol = block_reduce(pol, Add(), sf);
+  kl = block_reduce(kl, Add(), sf);
+  clip = block_reduce(clip, Add(), sf);
+  rs = block_reduce(rs, Add(), sf);
+  akl = block_reduce(akl, Add(), sf);
+  if (tid != 0) return;
+  const float invR = 1.0f / (float)p.R;
+  const float policy = pol * invR, klm = kl * invR;
+  const float loss = policy + p.beta * klm;
+  if (p.loss) p.loss[0] = loss;
+  if (!p.metrics) return;
+  double* m = p.metrics;
+  m[DSV41_GRPO_M_LOSS] = (double)loss;
+  m[DSV41_GRPO_M_POLICY_LOSS] = (double)policy;
+  m[DSV41_GRPO_M_KL] = (double)klm;
+  m[DSV41_GRPO_M_CLIP_FRACTION] = (double)(clip * invR);
+  m[DSV41_GRPO_M_IMPORTANCE_RATIO] = (double)(rs * invR);
+  m[DSV41_GRPO_M_APPROX_KL] = (double)(akl * invR);
+}
+
+int plan_grpo(const dsv41_grpo_desc* d, size_t* ws) {
+  if (!d) return fail(DSV41_E_INVALID, "GRPO descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_grpo_desc))
+    return fail(DSV41_E_ABI, "dsv41_grpo_desc size mismatch (rebuild the binding)");
+  if (d->n_responses <= 0 || d->n_tokens < 0)
+    return fail(DSV41_E_INVALID, "policy and behavior must contain the same nonzero number of responses");
+  if (!(isfinite(d->clip_eps) && d->clip_eps >= 0.0 && d->clip_eps < 1.0))
+    return fail(DSV41_E_INVALID, "clip_eps must be finite and in [0, 1)");
+  if (!(isfinite(d->kl_beta) && d->kl_beta >= 0.0)) return fail(DSV41_E_INVALID, "kl_beta must be finite and nonnegative");
+  if (d->kl_beta > 0.0 && !d->reference)
+    return fail(DSV41_E_INVALID, "positive kl_beta requires reference log probabilities");
+  if (!d->offsets || !d->current || !d->behavior || !d->advantages || !d->out_status)
+    return fail(DSV41_E_INVALID, "offsets, current, behavior, advantages and out_status are required");
+  *ws = (size_t)d->n_responses * sizeof(GPart);
+  return DSV41_OK;
+}
+
 int plan(const dsv41_token_tis_desc* d, size_t* ws) {
   if (!d) return fail(DSV41_E_INVALID, "Token-TIS descriptor is NULL");
   if (d->struct_size != sizeof(dsv41_token_tis_desc))
@@ -310,6 +450,43 @@ extern "C" int dsv41_token_tis_run(const dsv41_token_tis_desc* d, void* workspac
   hipLaunchKernelGGL(tis::response_kernel, dim3(p.R), dim3(tis::NT), 0, s, p);
   DSV41_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(tis::pool_kernel, dim3(1), dim3(tis::NT), 0, s, p);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
+}
+
+extern "C" size_t dsv41_grpo_workspace_bytes(const dsv41_grpo_desc* d) {
+  size_t ws = 0;
+  if (tis::plan_grpo(d, &ws) != DSV41_OK) return 0;
+  return ws;
+}
+
+extern "C" int dsv41_grpo_run(const dsv41_grpo_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  size_t need = 0;
+  int rc = tis::plan_grpo(d, &need);
+  if (rc != DSV41_OK) return rc;
+  if (!workspace || workspace_bytes < need) return fail(DSV41_E_WORKSPACE, "GRPO workspace is missing or too small");
+  tis::GParams p{};
+  p.off = d->offsets;
+  p.cur = d->current;
+  p.beh = d->behavior;
+  p.ref = d->kl_beta > 0.0 ? d->reference : nullptr;
+  p.adv = d->advantages;
+  p.eps = d->clip_eps;
+  p.lo = (float)(1.0 - d->clip_eps);
+  p.hi = (float)(1.0 + d->clip_eps);
+  p.epsf = (float)d->clip_eps;
+  p.beta = (float)d->kl_beta;
+  p.R = d->n_responses;
+  p.T = d->n_tokens;
+  p.part = static_cast<tis::GPart*>(workspace);
+  p.grad = d->out_grad;
+  p.status = d->out_status;
+  p.loss = d->out_loss;
+  p.metrics = d->out_metrics;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tis::grpo_response_kernel, dim3(p.R), dim3(tis::NT), 0, s, p);
+  DSV41_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tis::grpo_pool_kernel, dim3(1), dim3(tis::NT), 0, s, p);
   DSV41_HIP_CHECK(hipGetLastError());
   return DSV41_OK;
 }

@@ -133,12 +133,34 @@ class TokenTisDesc(ctypes.Structure):
     ]
 
 
+class GrpoDesc(ctypes.Structure):
+    """Mirror of dsv41_grpo_desc."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("n_responses", ctypes.c_int32),
+        ("n_tokens", ctypes.c_int64),
+        ("offsets", ctypes.c_void_p),
+        ("current", ctypes.c_void_p),
+        ("behavior", ctypes.c_void_p),
+        ("reference", ctypes.c_void_p),
+        ("advantages", ctypes.c_void_p),
+        ("clip_eps", ctypes.c_double),
+        ("kl_beta", ctypes.c_double),
+        ("out_loss", ctypes.c_void_p),
+        ("out_grad", ctypes.c_void_p),
+        ("out_metrics", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+    ]
+
+
 EXPORTS = (
     "dsv41_abi_version",
     "dsv41_sampler_desc_size",
     "dsv41_logprob_desc_size",
     "dsv41_logprob_grad_desc_size",
     "dsv41_token_tis_desc_size",
+    "dsv41_grpo_desc_size",
     "dsv41_last_error",
     "dsv41_sampler_workspace_bytes",
     "dsv41_sampler_run",
@@ -147,6 +169,8 @@ EXPORTS = (
     "dsv41_logprob_grad_run",
     "dsv41_token_tis_workspace_bytes",
     "dsv41_token_tis_run",
+    "dsv41_grpo_workspace_bytes",
+    "dsv41_grpo_run",
 )
 
 _lock = threading.Lock()
@@ -159,6 +183,7 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_logprob_desc_size.restype = ctypes.c_size_t
     lib.dsv41_logprob_grad_desc_size.restype = ctypes.c_size_t
     lib.dsv41_token_tis_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_grpo_desc_size.restype = ctypes.c_size_t
     lib.dsv41_last_error.restype = ctypes.c_char_p
     lib.dsv41_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.dsv41_sampler_workspace_bytes.argtypes = [ctypes.POINTER(SamplerDesc)]
@@ -177,6 +202,10 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_token_tis_run.restype = ctypes.c_int
     lib.dsv41_token_tis_run.argtypes = [ctypes.POINTER(TokenTisDesc), ctypes.c_void_p, ctypes.c_size_t,
                                         ctypes.c_void_p]
+    lib.dsv41_grpo_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsv41_grpo_workspace_bytes.argtypes = [ctypes.POINTER(GrpoDesc)]
+    lib.dsv41_grpo_run.restype = ctypes.c_int
+    lib.dsv41_grpo_run.argtypes = [ctypes.POINTER(GrpoDesc), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     return lib
 
 
@@ -201,6 +230,8 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("dsv41_logprob_grad_desc layout differs between library and binding")
         if lib.dsv41_token_tis_desc_size() != ctypes.sizeof(TokenTisDesc):
             raise RuntimeError("dsv41_token_tis_desc layout differs between library and binding")
+        if lib.dsv41_grpo_desc_size() != ctypes.sizeof(GrpoDesc):
+            raise RuntimeError("dsv41_grpo_desc layout differs between library and binding")
         _lib = lib
         return lib
 
