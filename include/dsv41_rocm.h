@@ -133,6 +133,45 @@ typedef struct dsv41_logprob_desc {
 } dsv41_logprob_desc;
 
 /*
+ * One GPU's slice of a vocabulary-sharded head (tensor-parallel lm_head): w holds the head's
+ * rows [vocab_offset, vocab_offset + vocab).  For each token, out_state[n] (16 bytes, the
+ * wire format of the sharded path) = (m, s, a, z_t) over this slice:
+ *   m = max_v z[n, v],  s = sum_v exp(z[n, v] - m),  a = sum_v exp(z[n, v] - m) * z[n, v],
+ *   z_t = z[n, targets[n]] when this slice holds targets[n], -inf otherwise.
+ * The states of all slices, gathered ([n_shards, N, 4]), combine exactly into the
+ * unsharded result with dsv41_logprob_combine_run.
+ */
+typedef struct dsv41_logprob_shard_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_logprob_shard_desc) */
+  int32_t n_tokens;
+  int32_t hidden;
+  int32_t vocab;          /* rows of this slice */
+  const void* x;          /* bf16 [N, H] */
+  int64_t x_row_stride;
+  const void* w;          /* bf16 [vocab, H]: this slice's rows */
+  int64_t w_row_stride;
+  const int64_t* targets; /* [N], global ids */
+  int64_t vocab_offset;   /* global id of w's first row */
+  float temperature;
+  float* out_state;       /* [N, 4] fp32 */
+} dsv41_logprob_shard_desc;
+
+/* Combines gathered shard states into the outputs of dsv41_logprob_run. */
+typedef struct dsv41_logprob_combine_desc {
+  uint32_t struct_size; /* = sizeof(dsv41_logprob_combine_desc) */
+  int32_t n_tokens;
+  int32_t n_shards;
+  const float* states;    /* [n_shards, N, 4], 16-byte aligned */
+  const float* behavior;  /* [N] or NULL */
+  float is_cap;
+  float* out_logprob;     /* [N] */
+  float* out_entropy;     /* [N] or NULL */
+  float* out_ratio;       /* [N] or NULL; requires behavior */
+  int32_t* out_status;    /* [N] or NULL */
+  float* out_lse;         /* [N] or NULL */
+} dsv41_logprob_combine_desc;
+
+/*
  * Gradient of a loss L(out_logprob, out_entropy) with respect to the logits, for the
  * vocabulary rows [vocab_begin, vocab_end):
  *   p = softmax(z[n]),  z = logits / temperature,
@@ -288,6 +327,8 @@ size_t dsv41_logprob_desc_size(void);
 size_t dsv41_logprob_grad_desc_size(void);
 size_t dsv41_token_tis_desc_size(void);
 size_t dsv41_grpo_desc_size(void);
+size_t dsv41_logprob_shard_desc_size(void);
+size_t dsv41_logprob_combine_desc_size(void);
 const char* dsv41_last_error(void);
 
 /* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch. */
@@ -299,6 +340,12 @@ int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t wo
 size_t dsv41_logprob_workspace_bytes(const dsv41_logprob_desc* desc);
 int dsv41_logprob_run(const dsv41_logprob_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream /* hipStream_t */);
+
+/* Vocabulary-sharded head: per-slice states, then the exact combine (no workspace). */
+size_t dsv41_logprob_shard_workspace_bytes(const dsv41_logprob_shard_desc* desc);
+int dsv41_logprob_shard_run(const dsv41_logprob_shard_desc* desc, void* workspace, size_t workspace_bytes,
+                            void* stream /* hipStream_t */);
+int dsv41_logprob_combine_run(const dsv41_logprob_combine_desc* desc, void* stream /* hipStream_t */);
 
 /* Gradient of the fused log-prob with respect to the logits (no workspace). */
 int dsv41_logprob_grad_run(const dsv41_logprob_grad_desc* desc, void* stream /* hipStream_t */);

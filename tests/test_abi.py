@@ -35,7 +35,8 @@ def test_library_exports_every_declared_function():
 def test_descriptor_layouts_match_header(tmp_path):
     fields = {"dsv41_sampler_desc": _lib.SamplerDesc, "dsv41_logprob_desc": _lib.LogprobDesc,
               "dsv41_logprob_grad_desc": _lib.LogprobGradDesc, "dsv41_token_tis_desc": _lib.TokenTisDesc,
-              "dsv41_grpo_desc": _lib.GrpoDesc}
+              "dsv41_grpo_desc": _lib.GrpoDesc,
+              "dsv41_logprob_shard_desc": _lib.LogprobShardDesc, "dsv41_logprob_combine_desc": _lib.LogprobCombineDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {", 'printf("{");']
     first = True
     for cname, cls in fields.items():

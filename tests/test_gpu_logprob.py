@@ -132,3 +132,31 @@ def test_custom_op_matches_wrapper():
     assert torch.max(torch.abs(lse.double() - (zt - lp.double()))).item() <= 1e-4
     lp2, _, empty, _ = torch.ops.dsv41_rocm.selected_log_probs(x, w, t, 0.9, None, 2.0)
     assert torch.equal(lp2, rlp) and empty.numel() == 0
+
+
+@pytest.mark.parametrize("n,h,v,cuts", [(512, 2048, 20000, [12000]), (300, 136, 1000, [1, 257, 700]),
+                                        (384, 7168, 129280, [16160 * k for k in range(1, 8)])])
+def test_vocabulary_shards_combine_to_the_unsharded_head(n, h, v, cuts):
+    """A vocabulary-sharded head on one GPU: each slice's 16-byte states, stacked as an
+    all-gather would deliver them, combine to the unsharded outputs."""
+    print(f"case: shards N={n} H={h} V={v} cuts={cuts}", flush=True)
+    from dsv41_rocm import combine_states, shard_states
+
+    g = torch.Generator(device=DEV).manual_seed(n + v)
+    x = torch.randn(n, h, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.3 * torch.randn(v, h, generator=g, device=DEV) / (h ** 0.5) * 8).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g, device=DEV)
+    behavior = torch.full((n,), -9.0, device=DEV)
+    lp, ent, ratio = selected_log_probs(x, w, t, 0.8, behavior=behavior)
+    bounds = [0] + cuts + [v]
+    states = torch.stack([shard_states(x, w[b:e], t, 0.8, b) for b, e in zip(bounds[:-1], bounds[1:])])
+    assert states.shape == (len(bounds) - 1, n, 4)
+    owned = torch.isfinite(states[:, :, 3]).sum(dim=0)
+    assert torch.equal(owned, torch.ones_like(owned))  # each target logit comes from exactly one slice
+    clp, cent, cratio = combine_states(states, behavior=behavior)
+    assert torch.max(torch.abs(clp - lp)).item() <= 2e-5
+    assert torch.max(torch.abs(cent - ent)).item() <= 2e-5
+    assert torch.max(torch.abs(cratio - ratio)).item() <= 2e-5
+    rlp, rent = reference(x, w, t, 0.8)
+    assert torch.max(torch.abs(clp.double() - rlp)).item() <= TOL
+    assert torch.max(torch.abs(cent.double() - rent)).item() <= TOL

@@ -425,13 +425,14 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 }
 
 struct MergeParams {
-  const float4* part;
+  const float4* part;  // [splits][N] split states, or [shards][N] shard states (combine)
   const uint16_t* x;
   int64_t xs;
   const uint16_t* w;
   int64_t ws;
   const int64_t* targets;
   int N, H, V, splits;
+  int64_t voff;  // shard: global id of w's first row
   float invT;
   const float* behavior;
   float is_cap;
@@ -440,47 +441,65 @@ struct MergeParams {
   float* ratio;
   int32_t* status;
   float* lse_out;
+  float4* state_out;  // shard: [N] merged states
 };
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
-// One wave per token: the target logit z_t = (x[n] . w[t_n]) / T as an fp32 dot product,
-// the exact merge of the per-split softmax states, then log-prob, entropy, the Token-TIS
-// weight and status.
+constexpr int MERGE_FINAL = 0;    // split states + target dot product -> log-prob, entropy, ratio
+constexpr int MERGE_STATE = 1;    // split states + target dot product -> one shard state per token
+constexpr int MERGE_COMBINE = 2;  // shard states (target logit inside) -> log-prob, entropy, ratio
+
+// One wave per token.  The target logit z_t = (x[n] . w[t_n]) / T is an fp32 dot product
+// (FINAL, and STATE when this shard holds row t_n; -inf otherwise); COMBINE takes it from the
+// shard that holds it.  The states merge exactly (associative LSE merge), then log-prob,
+// entropy, lse, the Token-TIS weight and status, or (STATE) the merged 16-byte state.
+template <int MODE>
 __global__ __launch_bounds__(256) void merge_kernel(MergeParams q) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= q.N) return;  // uniform per wave
-  const int64_t t = q.targets[n];
-  float zt = __builtin_nanf("");
-  if (t >= 0 && t < q.V) {
-    const uint4* xr = reinterpret_cast<const uint4*>(q.x + (int64_t)n * q.xs);
-    const uint4* wr = reinterpret_cast<const uint4*>(q.w + t * q.ws);
-    float d0 = 0.0f, d1 = 0.0f;
-    for (int c = lane; c < q.H / 8; c += 64) {
-      const uint4 xv = xr[c], wv = wr[c];
-      d0 = __builtin_fmaf(bf16_lo(xv.x), bf16_lo(wv.x), d0);
-      d1 = __builtin_fmaf(bf16_hi(xv.x), bf16_hi(wv.x), d1);
-      d0 = __builtin_fmaf(bf16_lo(xv.y), bf16_lo(wv.y), d0);
-      d1 = __builtin_fmaf(bf16_hi(xv.y), bf16_hi(wv.y), d1);
-      d0 = __builtin_fmaf(bf16_lo(xv.z), bf16_lo(wv.z), d0);
-      d1 = __builtin_fmaf(bf16_hi(xv.z), bf16_hi(wv.z), d1);
-      d0 = __builtin_fmaf(bf16_lo(xv.w), bf16_lo(wv.w), d0);
-      d1 = __builtin_fmaf(bf16_hi(xv.w), bf16_hi(wv.w), d1);
+  float zt = MODE == MERGE_STATE ? NEG_INF : __builtin_nanf("");
+  if (MODE != MERGE_COMBINE) {
+    const int64_t t = q.targets[n] - q.voff;
+    if (t >= 0 && t < q.V) {
+      const uint4* xr = reinterpret_cast<const uint4*>(q.x + (int64_t)n * q.xs);
+      const uint4* wr = reinterpret_cast<const uint4*>(q.w + t * q.ws);
+      float d0 = 0.0f, d1 = 0.0f;
+      for (int c = lane; c < q.H / 8; c += 64) {
+        const uint4 xv = xr[c], wv = wr[c];
+        d0 = __builtin_fmaf(bf16_lo(xv.x), bf16_lo(wv.x), d0);
+        d1 = __builtin_fmaf(bf16_hi(xv.x), bf16_hi(wv.x), d1);
+        d0 = __builtin_fmaf(bf16_lo(xv.y), bf16_lo(wv.y), d0);
+        d1 = __builtin_fmaf(bf16_hi(xv.y), bf16_hi(wv.y), d1);
+        d0 = __builtin_fmaf(bf16_lo(xv.z), bf16_lo(wv.z), d0);
+        d1 = __builtin_fmaf(bf16_hi(xv.z), bf16_hi(wv.z), d1);
+        d0 = __builtin_fmaf(bf16_lo(xv.w), bf16_lo(wv.w), d0);
+        d1 = __builtin_fmaf(bf16_hi(xv.w), bf16_hi(wv.w), d1);
+      }
+      zt = wave_sum(d0 + d1) * q.invT;
     }
-    zt = wave_sum(d0 + d1) * q.invT;
   }
-  float m = NEG_INF, s = 0.0f, a = 0.0f;
+  float m = NEG_INF, s = 0.0f, a = 0.0f, zs = NEG_INF;
   for (int k = lane; k < q.splits; k += 64) {
     const float4 o = q.part[(int64_t)k * q.N + n];
     merge(m, s, a, o.x, o.y, o.z);
+    if (MODE == MERGE_COMBINE) zs = fmaxf(zs, o.w);
   }
   const float mx = wave_max(m);
   const float c = m == NEG_INF ? 0.0f : exp2f((m - mx) * LOG2E);
   s = wave_sum(s * c);
   a = wave_sum(a * c);
+  if (MODE == MERGE_COMBINE) {
+    zs = wave_max(zs);
+    zt = zs > NEG_INF ? zs : __builtin_nanf("");  // no shard held the target
+  }
   if (lane != 0) return;
+  if (MODE == MERGE_STATE) {
+    q.state_out[n] = make_float4(mx, s, a, zt);
+    return;
+  }
   const float lse = mx + logf(s);
   const float lp = zt - lse;
   const float ent = lse - a / s;
@@ -676,7 +695,118 @@ extern "C" int dsv41_logprob_run(const dsv41_logprob_desc* d, void* workspace, s
   q.ratio = d->out_ratio;
   q.status = d->out_status;
   q.lse_out = d->out_lse;
-  hipLaunchKernelGGL(merge_kernel, dim3((d->n_tokens + 3) / 4), dim3(256), 0, s, q);
+  hipLaunchKernelGGL(merge_kernel<MERGE_FINAL>, dim3((d->n_tokens + 3) / 4), dim3(256), 0, s, q);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
+}
+
+// ---------------------------------------------------------------- vocabulary shards
+// One GPU's slice of a vocabulary-sharded head: the forward's kernels over the slice, with
+// the split states merged into one 16-byte state per token, (max z, sum e, sum e*z, z_t),
+// z_t = -inf unless this slice holds the target.  States of all slices, gathered, go to
+// dsv41_logprob_combine_run.
+namespace {
+int shard_plan(const dsv41_logprob_shard_desc* d, dsv41_logprob_desc* fd, Plan* pl) {
+  if (!d) return fail(DSV41_E_INVALID, "log-prob shard descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_logprob_shard_desc))
+    return fail(DSV41_E_ABI, "dsv41_logprob_shard_desc size mismatch (rebuild the binding)");
+  if (d->vocab_offset < 0) return fail(DSV41_E_INVALID, "vocab_offset must be nonnegative");
+  if (d->n_tokens > 0 && !d->out_state) return fail(DSV41_E_INVALID, "out_state is required");
+  *fd = dsv41_logprob_desc{};
+  fd->struct_size = sizeof(dsv41_logprob_desc);
+  fd->n_tokens = d->n_tokens;
+  fd->hidden = d->hidden;
+  fd->vocab = d->vocab;
+  fd->x = d->x;
+  fd->x_row_stride = d->x_row_stride;
+  fd->w = d->w;
+  fd->w_row_stride = d->w_row_stride;
+  fd->targets = d->targets;
+  fd->temperature = d->temperature;
+  fd->out_logprob = d->out_state;  // non-null marker for the shared checks
+  return plan(fd, pl);
+}
+}  // namespace
+
+extern "C" size_t dsv41_logprob_shard_workspace_bytes(const dsv41_logprob_shard_desc* d) {
+  dsv41_logprob_desc fd;
+  Plan pl;
+  if (shard_plan(d, &fd, &pl) != DSV41_OK) return 0;
+  return pl.workspace;
+}
+
+extern "C" int dsv41_logprob_shard_run(const dsv41_logprob_shard_desc* d, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  dsv41_logprob_desc fd;
+  Plan pl;
+  int rc = shard_plan(d, &fd, &pl);
+  if (rc != DSV41_OK) return rc;
+  if (d->n_tokens == 0) return DSV41_OK;
+  if (!workspace || workspace_bytes < pl.workspace)
+    return fail(DSV41_E_WORKSPACE, "log-prob workspace is missing or too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Params p{};
+  p.x = static_cast<const uint16_t*>(d->x);
+  p.xs = d->x_row_stride;
+  p.w = static_cast<const uint16_t*>(d->w);
+  p.ws = d->w_row_stride;
+  p.targets = d->targets;
+  p.part = static_cast<float4*>(workspace);
+  p.N = d->n_tokens;
+  p.H = d->hidden;
+  p.V = d->vocab;
+  p.invT = 1.0f / d->temperature;
+  p.splits = pl.splits;
+  p.n_vb = pl.n_vb;
+  p.n_tb = pl.n_tb;
+  p.group_t = pl.group_t;
+  p.group_s = pl.group_s;
+  hipLaunchKernelGGL(fused_kernel<false>, dim3(pl.n_tb * pl.splits), dim3(NT), 0, s, p);
+  DSV41_HIP_CHECK(hipGetLastError());
+  MergeParams q{};
+  q.part = p.part;
+  q.x = p.x;
+  q.xs = p.xs;
+  q.w = p.w;
+  q.ws = p.ws;
+  q.targets = d->targets;
+  q.N = d->n_tokens;
+  q.H = d->hidden;
+  q.V = d->vocab;
+  q.splits = pl.splits;
+  q.voff = d->vocab_offset;
+  q.invT = p.invT;
+  q.state_out = reinterpret_cast<float4*>(d->out_state);
+  hipLaunchKernelGGL(merge_kernel<MERGE_STATE>, dim3((d->n_tokens + 3) / 4), dim3(256), 0, s, q);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
+}
+
+extern "C" int dsv41_logprob_combine_run(const dsv41_logprob_combine_desc* d, void* stream) {
+  if (!d) return fail(DSV41_E_INVALID, "log-prob combine descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_logprob_combine_desc))
+    return fail(DSV41_E_ABI, "dsv41_logprob_combine_desc size mismatch (rebuild the binding)");
+  if (d->n_tokens < 0 || d->n_shards <= 0) return fail(DSV41_E_INVALID, "need at least one shard and n_tokens >= 0");
+  if (d->n_tokens > 0 && (!d->states || !d->out_logprob))
+    return fail(DSV41_E_INVALID, "states and out_logprob are required");
+  if (((uintptr_t)d->states) % 16) return fail(DSV41_E_INVALID, "states must be 16-byte aligned");
+  if (d->out_ratio && !d->behavior) return fail(DSV41_E_INVALID, "ratio output requires behavior log-probs");
+  if (d->behavior && !(isfinite(d->is_cap) && d->is_cap > 0.0f))
+    return fail(DSV41_E_INVALID, "is_cap must be finite and positive");
+  if (d->n_tokens == 0) return DSV41_OK;
+  MergeParams q{};
+  q.part = reinterpret_cast<const float4*>(d->states);
+  q.N = d->n_tokens;
+  q.splits = d->n_shards;
+  q.behavior = d->behavior;
+  q.is_cap = d->is_cap;
+  q.lp = d->out_logprob;
+  q.ent = d->out_entropy;
+  q.ratio = d->out_ratio;
+  q.status = d->out_status;
+  q.lse_out = d->out_lse;
+  hipLaunchKernelGGL(merge_kernel<MERGE_COMBINE>, dim3((d->n_tokens + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), q);
   DSV41_HIP_CHECK(hipGetLastError());
   return DSV41_OK;
 }

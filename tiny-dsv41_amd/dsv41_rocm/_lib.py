@@ -154,6 +154,43 @@ class GrpoDesc(ctypes.Structure):
     ]
 
 
+class LogprobShardDesc(ctypes.Structure):
+    """Mirror of dsv41_logprob_shard_desc."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("n_tokens", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("x_row_stride", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("w_row_stride", ctypes.c_int64),
+        ("targets", ctypes.c_void_p),
+        ("vocab_offset", ctypes.c_int64),
+        ("temperature", ctypes.c_float),
+        ("out_state", ctypes.c_void_p),
+    ]
+
+
+class LogprobCombineDesc(ctypes.Structure):
+    """Mirror of dsv41_logprob_combine_desc."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("n_tokens", ctypes.c_int32),
+        ("n_shards", ctypes.c_int32),
+        ("states", ctypes.c_void_p),
+        ("behavior", ctypes.c_void_p),
+        ("is_cap", ctypes.c_float),
+        ("out_logprob", ctypes.c_void_p),
+        ("out_entropy", ctypes.c_void_p),
+        ("out_ratio", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+        ("out_lse", ctypes.c_void_p),
+    ]
+
+
 EXPORTS = (
     "dsv41_abi_version",
     "dsv41_sampler_desc_size",
@@ -161,6 +198,8 @@ EXPORTS = (
     "dsv41_logprob_grad_desc_size",
     "dsv41_token_tis_desc_size",
     "dsv41_grpo_desc_size",
+    "dsv41_logprob_shard_desc_size",
+    "dsv41_logprob_combine_desc_size",
     "dsv41_last_error",
     "dsv41_sampler_workspace_bytes",
     "dsv41_sampler_run",
@@ -171,6 +210,9 @@ EXPORTS = (
     "dsv41_token_tis_run",
     "dsv41_grpo_workspace_bytes",
     "dsv41_grpo_run",
+    "dsv41_logprob_shard_workspace_bytes",
+    "dsv41_logprob_shard_run",
+    "dsv41_logprob_combine_run",
 )
 
 _lock = threading.Lock()
@@ -184,6 +226,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_logprob_grad_desc_size.restype = ctypes.c_size_t
     lib.dsv41_token_tis_desc_size.restype = ctypes.c_size_t
     lib.dsv41_grpo_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_logprob_shard_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_logprob_combine_desc_size.restype = ctypes.c_size_t
     lib.dsv41_last_error.restype = ctypes.c_char_p
     lib.dsv41_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.dsv41_sampler_workspace_bytes.argtypes = [ctypes.POINTER(SamplerDesc)]
@@ -206,6 +250,13 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_grpo_workspace_bytes.argtypes = [ctypes.POINTER(GrpoDesc)]
     lib.dsv41_grpo_run.restype = ctypes.c_int
     lib.dsv41_grpo_run.argtypes = [ctypes.POINTER(GrpoDesc), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.dsv41_logprob_shard_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsv41_logprob_shard_workspace_bytes.argtypes = [ctypes.POINTER(LogprobShardDesc)]
+    lib.dsv41_logprob_shard_run.restype = ctypes.c_int
+    lib.dsv41_logprob_shard_run.argtypes = [ctypes.POINTER(LogprobShardDesc), ctypes.c_void_p, ctypes.c_size_t,
+                                            ctypes.c_void_p]
+    lib.dsv41_logprob_combine_run.restype = ctypes.c_int
+    lib.dsv41_logprob_combine_run.argtypes = [ctypes.POINTER(LogprobCombineDesc), ctypes.c_void_p]
     return lib
 
 
@@ -232,6 +283,10 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("dsv41_token_tis_desc layout differs between library and binding")
         if lib.dsv41_grpo_desc_size() != ctypes.sizeof(GrpoDesc):
             raise RuntimeError("dsv41_grpo_desc layout differs between library and binding")
+        if lib.dsv41_logprob_shard_desc_size() != ctypes.sizeof(LogprobShardDesc):
+            raise RuntimeError("dsv41_logprob_shard_desc layout differs between library and binding")
+        if lib.dsv41_logprob_combine_desc_size() != ctypes.sizeof(LogprobCombineDesc):
+            raise RuntimeError("dsv41_logprob_combine_desc layout differs between library and binding")
         _lib = lib
         return lib
 

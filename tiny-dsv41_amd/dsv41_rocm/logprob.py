@@ -236,6 +236,80 @@ def selected_log_probs(
     return lp, ent, ratio
 
 
+def shard_states(hidden: torch.Tensor, weight_slice: torch.Tensor, targets: torch.Tensor, temperature: float,
+                 vocab_offset: int) -> torch.Tensor:
+    """One GPU's part of a vocabulary-sharded head: ``weight_slice`` holds the head's rows
+    ``[vocab_offset, vocab_offset + rows)``.  Returns fp32 ``[N, 4]`` states
+    ``(max z, sum e, sum e*z, z_target or -inf)``, 16 bytes per token: what a tensor-parallel
+    head exchanges (one all-gather) before ``combine_states``."""
+    if not isinstance(vocab_offset, int) or vocab_offset < 0:
+        raise ValueError("vocab_offset must be a nonnegative integer")
+    if not math.isfinite(temperature) or temperature <= 0:
+        raise ValueError("temperature must be finite and positive")
+    if hidden.ndim != 2 or weight_slice.ndim != 2 or hidden.shape[1] != weight_slice.shape[1]:
+        raise ValueError("hidden must be [tokens, hidden] and weight [vocab, hidden]")
+    if not (hidden.is_cuda and weight_slice.is_cuda):
+        raise ValueError("hidden and weight must be on the GPU (libdsv41hip has no CPU path)")
+    n, h = hidden.shape
+    if h % 8:
+        raise ValueError("hidden size must be a multiple of 8")
+    hidden = hidden.to(torch.bfloat16)
+    weight_slice = weight_slice.to(torch.bfloat16)
+    if hidden.stride(1) != 1 or hidden.stride(0) % 8 or hidden.data_ptr() % 16:
+        hidden = hidden.contiguous()
+    if weight_slice.stride(1) != 1 or weight_slice.stride(0) % 8 or weight_slice.data_ptr() % 16:
+        weight_slice = weight_slice.contiguous()
+    targets = targets.to(device=hidden.device, dtype=torch.int64).reshape(-1).contiguous()
+    if targets.numel() != n:
+        raise ValueError("one target is required per token")
+    states = torch.empty(n, 4, dtype=torch.float32, device=hidden.device)
+    d = _lib.LogprobShardDesc()
+    d.struct_size = ctypes.sizeof(_lib.LogprobShardDesc)
+    d.n_tokens, d.hidden, d.vocab = n, h, weight_slice.shape[0]
+    d.x, d.x_row_stride = hidden.data_ptr(), hidden.stride(0)
+    d.w, d.w_row_stride = weight_slice.data_ptr(), weight_slice.stride(0)
+    d.targets, d.vocab_offset, d.temperature = targets.data_ptr(), vocab_offset, temperature
+    d.out_state = states.data_ptr()
+    lib = _lib.load()
+    ws_bytes = lib.dsv41_logprob_shard_workspace_bytes(ctypes.byref(d))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=hidden.device)
+    with torch.cuda.device(hidden.device):
+        rc = lib.dsv41_logprob_shard_run(ctypes.byref(d), workspace.data_ptr(), ws_bytes,
+                                         torch.cuda.current_stream(hidden.device).cuda_stream)
+    _lib.check(rc)
+    return states
+
+
+def combine_states(states: torch.Tensor, *, behavior: Optional[torch.Tensor] = None, is_cap: float = 2.0,
+                   check: bool = True) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Exact combine of gathered shard states ``[shards, N, 4]`` into ``(logprob, entropy,
+    ratio or None)``, the outputs ``selected_log_probs`` gives for the unsharded head."""
+    if states.ndim != 3 or states.shape[2] != 4 or not states.is_cuda:
+        raise ValueError("states must be a GPU tensor of shape [shards, tokens, 4]")
+    states = states.to(torch.float32).contiguous()
+    g, n, _ = states.shape
+    dev = states.device
+    lp = torch.empty(n, dtype=torch.float32, device=dev)
+    ent = torch.empty(n, dtype=torch.float32, device=dev)
+    status = torch.empty(n, dtype=torch.int32, device=dev)
+    ratio = None
+    d = _lib.LogprobCombineDesc()
+    d.struct_size = ctypes.sizeof(_lib.LogprobCombineDesc)
+    d.n_tokens, d.n_shards, d.states = n, g, states.data_ptr()
+    if behavior is not None:
+        behavior = behavior.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        ratio = torch.empty(n, dtype=torch.float32, device=dev)
+        d.behavior, d.is_cap, d.out_ratio = behavior.data_ptr(), is_cap, ratio.data_ptr()
+    d.out_logprob, d.out_entropy, d.out_status = lp.data_ptr(), ent.data_ptr(), status.data_ptr()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.dsv41_logprob_combine_run(ctypes.byref(d), torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(rc)
+    if check and n and bool((status != 0).any()):
+        _status_error(status)
+    return lp, ent, ratio
+
+
 def score_targets(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
                   temperature: float) -> torch.Tensor:
     """Drop-in for native_lora.py:80-82 (``_score_targets``): fp32 log-probs [N]."""
