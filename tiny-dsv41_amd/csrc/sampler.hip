@@ -781,7 +781,7 @@ __device__ __forceinline__ Hist hist_tables(unsigned char* smem, const Layout& L
 // ====================================================================== FULL
 // No truncation: kept set = whole vocabulary.  Chunk c = [c*64G, (c+1)*64G) is one
 // wave's span of one tile; its (max, sum exp(z - max)) go to LDS.
-template <typename TIn, int G, bool VEC>
+template <typename TIn, int G, bool VEC, bool RACE>
 __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -860,7 +860,8 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   for (int s = tid; s < U; s += NT) atomicAdd(&cs[h.tok[s] / (64 * G)], exp2f((penz[s] - M) * LOG2E));
   __syncthreads();
 
-  if (p.exps && !p.greedy) {
+  if (RACE && !p.greedy) {
+    // (a separate instantiation: the race's registers would cost the inverse-CDF draw occupancy)
     // Exponential race: the token is argmax_i p_i / E_i with p_i = exp(log_softmax(z)_i),
     // each step in fp32 as torch forms it (log_softmax = z - (max + log(sum)), exp,
     // division), first index on ties.  This is torch.multinomial(p, 1) on the CPU fed the
@@ -1814,10 +1815,16 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   const bool bf = pl.esize == 2;
   switch (pl.mode) {
     case MODE_FULL:
-      if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true>, FULL_NT, pl.lds, d->rows, p, s)
-                            : launch(full_kernel<uint16_t, 8, false>, FULL_NT, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(full_kernel<float, 4, true>, FULL_NT, pl.lds, d->rows, p, s)
-                    : launch(full_kernel<float, 4, false>, FULL_NT, pl.lds, d->rows, p, s);
+      if (p.exps) {
+        if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, true>, FULL_NT, pl.lds, d->rows, p, s)
+                              : launch(full_kernel<uint16_t, 8, false, true>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 4, true, true>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 4, false, true>, FULL_NT, pl.lds, d->rows, p, s);
+      }
+      if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, false>, FULL_NT, pl.lds, d->rows, p, s)
+                            : launch(full_kernel<uint16_t, 8, false, false>, FULL_NT, pl.lds, d->rows, p, s);
+      return pl.vec ? launch(full_kernel<float, 4, true, false>, FULL_NT, pl.lds, d->rows, p, s)
+                    : launch(full_kernel<float, 4, false, false>, FULL_NT, pl.lds, d->rows, p, s);
     case MODE_TOPK:
       if (bf) return pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
                             : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
