@@ -179,6 +179,31 @@ def test_status_nonfinite_bad_history_bad_uniform():
         sample(logits.to(DEV), uniforms=u.clamp(max=0.9).to(DEV))
 
 
+def test_nonfinite_history_tokens_and_penalty_overflow():
+    """NaN, +inf and -inf on history tokens, a -inf elsewhere, and a finite logit that
+    only overflows once the repetition penalty multiplies it, under lowering penalties
+    (history met in the stream, with and without counts) and under raising ones
+    (history gathered)."""
+    g = torch.Generator().manual_seed(9)
+    rows, V = 6, 9000
+    logits = torch.randn(rows, V, generator=g)
+    hist = torch.randint(0, V, (rows, 40), generator=g)
+    h0 = hist[:, 0]
+    logits[0, h0[0]] = float("nan")
+    logits[1, h0[1]] = float("inf")
+    logits[2, h0[2]] = float("-inf")
+    logits[3, h0[3]] = -3e38  # x * 1.5 overflows; x / T does not
+    logits[4, 5] = float("-inf")
+    u = torch.rand(rows, generator=g)
+    for knobs in (dict(repetition_penalty=1.5, top_k=20),
+                  dict(repetition_penalty=1.5, frequency_penalty=0.2, top_k=20, min_p=0.1),
+                  dict(repetition_penalty=0.7, presence_penalty=-0.2, top_k=20)):
+        gpu, ora = run_both(logits, u, hist, **knobs)
+        np.testing.assert_array_equal(gpu[3], ora[3])
+        assert all(gpu[3][r] & 1 for r in (0, 1, 2, 4)) and not gpu[3][5] & 1
+        assert_exact(gpu, ora)
+
+
 def test_repeatable_bitwise():
     inp = workloads.sampler_inputs("E", rows=32)
     args = dict(uniforms=inp["uniforms"].to(DEV), history=inp["history"].to(DEV), **inp["knobs"])

@@ -76,6 +76,7 @@ struct Params {
   double log_min_p;
   float T, rT, rp, pres, freq, top_p, min_p, lmin_f;
   int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words, cap;
+  int pen_lowers;  // penalties can only lower a logit: rp >= 1, presence >= 0, frequency >= 0
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -469,9 +470,11 @@ __device__ __forceinline__ void load_history(const Params& p, int row, HistIds<H
   hi.hl = max(0, min(hl, (int)p.hstride));
 }
 
-// Builds the tables; returns the number of slots (distinct in-vocabulary ids).
+// Builds the tables; returns the number of slots (distinct in-vocabulary ids).  With
+// counts false only the membership bitmap is built and 0 is returned.
 template <int NT, int HR>
-__device__ __forceinline__ int build_history(const Params& p, int row, const HistIds<HR>& hi, const Hist& h, Misc* m) {
+__device__ __forceinline__ int build_history(const Params& p, int row, const HistIds<HR>& hi, const Hist& h, Misc* m,
+                                             bool counts = true) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int W = p.words;
@@ -497,6 +500,7 @@ __device__ __forceinline__ int build_history(const Params& p, int row, const His
   }
   if (bad) atomicOr(&m->status, ST_BAD_HISTORY);
   __syncthreads();
+  if (!counts) return 0;
   const int per = (W + NT - 1) / NT;
   const int b = tid * per, e = min(b + per, W);
   int s = 0;
@@ -635,24 +639,6 @@ __device__ __forceinline__ void make_z(const float (&x)[G], int base, const Para
   }
 }
 
-// Raw logits with history tokens and (TAIL) indices >= V set to -inf.  Non-finite
-// raw logits are collected into the wave mask nf; ax tracks the largest |x|.
-template <int G, bool TAIL>
-__device__ __forceinline__ void mask_x(const float (&x)[G], int base, const Params& p,
-                                       const uint32_t* bitmap, float (&xm)[G], unsigned long long& nf,
-                                       float& ax) {
-  uint32_t pen = 0;
-  if (p.has_pen && (!TAIL || base < p.V)) pen = (bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u);
-#pragma unroll
-  for (int j = 0; j < G; ++j) {
-    nf |= __ballot(!isfinite(x[j]));  // positions >= V read as 0 and never count
-    ax = fmaxf(ax, fabsf(x[j]));
-    const uint32_t msk = 0u - ((pen >> j) & 1u);
-    xm[j] = __uint_as_float((msk & NEG_INF_BITS) | (~msk & __float_as_uint(x[j])));
-    if (TAIL && base + j >= p.V) xm[j] = NEG_INF;
-  }
-}
-
 // Adjacent floats (IEEE order; -0 is treated as +0; infinities and NaN map to themselves
 // where no neighbour exists).
 __device__ __forceinline__ float next_up(float x) {
@@ -690,12 +676,29 @@ __device__ __forceinline__ float pen_z(float x, uint32_t c, const Params& p) {
   return penalize(x, c, p) / p.T;
 }
 
+// An empty instruction that reads v.  Where a path never uses a loaded value, the
+// compiler's wait analysis still counts the load as pending on that path and makes the
+// next write of the register (the next batch's load) wait for every older load; reading
+// the value here ends that on every path.
+template <typename T>
+__device__ __forceinline__ void landed(T v) {
+  asm volatile("" ::"v"(v));
+}
+template <int HR>
+__device__ __forceinline__ void landed(const HistIds<HR>& hi) {
+#pragma unroll
+  for (int j = 0; j < HR; ++j) landed(hi.id[j]);
+}
+
 // Pipelined row stream.  `setup()` builds the history tables while the first batch
 // is in flight and returns the slot count.  `batch(t0, nt, R, s0, n, gx)` processes
 // tiles [t0, t0+PF) (TILE = NT*G elements each; tiles >= nt read as zeros) from the
 // raw registers R, together with the history slots [s0, s0+n) whose tokens lie in
 // those tiles: thread i holds the raw logit of slot s0+i in gx (for i < NT).
-template <typename TIn, int G, int NT, bool VEC, class Setup, class Batch>
+// LOWERING: the caller meets history tokens in the stream itself when p.pen_lowers is
+// set, and the gather is off then (a compile-time switch: an extra runtime flag costs
+// full_kernel the scalar registers that keep it at two workgroups per CU).
+template <typename TIn, int G, int NT, bool VEC, bool LOWERING, class Setup, class Batch>
 __device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc_t rs, const Hist& h,
                                            Setup setup, Batch batch) {
   constexpr int TILE = NT * G;
@@ -706,7 +709,7 @@ __device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc
   for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(A[k], rs, k * TILE + tid * G);
   const int U = setup();
   auto gather = [&](int t0, int& s0, int& n) -> float {
-    if (!p.has_pen) {
+    if (!p.has_pen || (LOWERING && p.pen_lowers)) {
       s0 = 0;
       n = 0;
       return 0.0f;
@@ -801,12 +804,13 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   constexpr int TILE = NT * G;
   int bad = 0;
   int U = 0;
-  stream_row<TIn, G, NT, VEC>(
+  stream_row<TIn, G, NT, VEC, false>(
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
         __syncthreads();
         if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
       [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
@@ -1085,6 +1089,17 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
 }
 
 // ====================================================================== TOPK
+// Wave-uniform values moved to scalar registers (they come from LDS or lane
+// reductions, which leave them in vector registers).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uni(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ uint64_t uni(uint64_t v) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
+
 // Keeps the candidate buffer at its top_k and within the min-p bound of mrun (a lower
 // bound of the row maximum); returns the new count and updates tau / tau_key.
 template <int NT>
@@ -1098,9 +1113,9 @@ __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, cons
     for (int i = tid; i < n; i += NT) e += minp_ok(ckey_z(cand[i]), mrun, p) ? 1 : 0;
     el = block_sum_i<NT>(e, m);
   }
-  const int keep = min(el, p.top_k);
+  const int keep = uni(min(el, p.top_k));
   if (keep == p.top_k && keep > 0) {
-    tau_key = cand[keep - 1];
+    tau_key = uni(cand[keep - 1]);
     tau = ckey_z(tau_key);
   }
   __syncthreads();
@@ -1254,7 +1269,6 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   float wm = NEG_INF;       // this wave's running maximum (a lower bound of the row max)
   float mblk = NEG_INF;     // all waves' running maxima at the last exchange
   int par = 0;
-  unsigned long long nfx = 0;  // lanes that saw a non-finite raw logit
   float ax = 0.0f;             // largest |x| seen by this lane
   float c_tau = __builtin_nanf(""), c_bnd = __builtin_nanf(""), c_thr = NEG_INF;  // x-threshold cache
 
@@ -1276,7 +1290,9 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
       if (i < wid) before += v;
       mb = fmaxf(mb, m->wmax[par][i]);
     }
-    mblk = mb;
+    mblk = uni(mb);
+    total = uni(total);
+    before = uni(before);
     par ^= 1;
     if (count + total > p.cap) count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key);
     return count + total <= p.cap ? count + before : -1;
@@ -1313,33 +1329,23 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   };
 
   int U = 0;
-  stream_row<TIn, G, NT, VEC>(
+  stream_row<TIn, G, NT, VEC, true>(  // lowering penalties: history tokens are met in the stream
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
         __syncthreads();
-        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        // with lowering penalties the stream evaluates history tokens itself and needs
+        // their counts only for a frequency penalty
+        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m, !p.pen_lowers || p.freq != 0.0f);
+        landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
       [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
-        float xm[PF][G];
-        float lx = NEG_INF;
+        // Tiles past the row are read and masked, not skipped, so that every load is
+        // consumed (as in full_kernel).
+        float x[PF][G];
 #pragma unroll
-        for (int k = 0; k < PF; ++k) {
-          const int t = t0 + k;
-          if (t < nt) {
-            const int base = t * TILE + tid * G;
-            float x[G];
-            unpack(R[k], x);
-            if ((t + 1) * TILE <= p.V) mask_x<G, false>(x, base, p, h.bitmap, xm[k], nfx, ax);
-            else mask_x<G, true>(x, base, p, h.bitmap, xm[k], nfx, ax);
-          } else {
-#pragma unroll
-            for (int j = 0; j < G; ++j) xm[k][j] = NEG_INF;
-          }
-#pragma unroll
-          for (int j = 0; j < G; ++j) lx = fmaxf(lx, xm[k][j]);
-        }
+        for (int k = 0; k < PF; ++k) unpack(R[k], x[k]);
         // the batch's first NT history slots, penalized exactly
         float zg = NEG_INF;
         uint32_t tg = 0;
@@ -1348,29 +1354,98 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
           tg = h.tok[s];
           zg = pen_z(gx, count_of(h, s), p);
           if (!isfinite(zg)) bad = 1;
+        } else {
+          landed(gx);
         }
-        // RN(x/T) is non-decreasing in x, so the largest z is the quotient of the largest x
-        const float lz = lx > NEG_INF ? lx / p.T : NEG_INF;
-        wm = fmaxf(wm, wave_max_dpp(fmaxf(lz, zg)));
+        float zmx = zg;
+        // A wave without a running maximum takes one from this batch's non-history
+        // logits before filtering, so that min-p already thins its first batch.
+        if (p.min_p > 0.0f && !(fmaxf(wm, mblk) > NEG_INF)) {
+          float lx = NEG_INF;
+#pragma unroll
+          for (int k = 0; k < PF; ++k) {
+            const int base = (t0 + k) * TILE + tid * G;
+            const uint32_t pen = p.has_pen && base < p.V ? (h.bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u) : 0u;
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+              if (base + j < p.V && !((pen >> j) & 1u)) lx = fmaxf(lx, x[k][j]);
+          }
+          // RN(x/T) is non-decreasing in x: the largest z is the quotient of the largest x
+          if (lx > NEG_INF) zmx = fmaxf(zmx, lx / p.T);
+        }
+        wm = uni(fmaxf(wm, wave_max_dpp(zmx)));
         const float bnd = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
         if (!(tau == c_tau && bnd == c_bnd)) {
           c_tau = tau;
           c_bnd = bnd;
-          c_thr = x_threshold(tau, bnd, p);
+          c_thr = uni(x_threshold(tau, bnd, p));
         }
         const float th = c_thr;
         const uint64_t tk = tau_key;
-        // stream elements: later tiles hold larger indices, so z > tau suffices against
-        // the k-th key; history tokens arrive out of order and compare full keys
+        // Stream elements: one compare per logit against the raw threshold; the test
+        // !(x < th) also passes NaN.  Later tiles hold larger indices, so z > tau
+        // suffices against the k-th key; history tokens compare full keys.  |x| is
+        // tracked for infinities and for x / T overflow, checked after the stream.
         unsigned long long bal[NE];
-        uint32_t wn = 0;
+        unsigned long long any = 0;
 #pragma unroll
         for (int k = 0; k < PF; ++k)
 #pragma unroll
           for (int j = 0; j < G; ++j) {
-            bal[k * G + j] = __ballot(xm[k][j] >= th);
-            wn += (uint32_t)__popcll(bal[k * G + j]);
+            ax = fmaxf(ax, fabsf(x[k][j]));
+            bal[k * G + j] = __ballot(!(x[k][j] < th));
+            any |= bal[k * G + j];
           }
+        if (any) {
+          // Passers are rare once the thresholds settle.  Positions past the row drop
+          // out and a non-finite logit flags the row.  The passers' z replaces x in
+          // place.  A history token under lowering penalties has z = pen_z(x) <= x / T,
+          // so it can only qualify when x passes: its exact z takes the full test here.
+          // Otherwise history tokens drop out and the gather brings their exact values.
+          // Every element above the running maximum passes, so the passers' largest z
+          // keeps that maximum exact.
+          float pz = NEG_INF;
+#pragma unroll
+          for (int k = 0; k < PF; ++k) {
+            const int base = (t0 + k) * TILE + tid * G;
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+              const int e = k * G + j;
+              if (bal[e]) {
+                bool ok = (bal[e] >> lane) & 1ull;
+                if (ok) {
+                  const int idx = base + j;
+                  const float xv = x[k][j];
+                  const bool in = idx < p.V;
+                  if (in && !isfinite(xv)) bad = 1;
+                  ok = in && isfinite(xv);
+                  if (ok) {
+                    if (p.has_pen && ((h.bitmap[idx >> 5] >> (idx & 31)) & 1u)) {
+                      if (p.pen_lowers) {
+                        const float z = pen_z(xv, p.freq != 0.0f ? count_of(h, slot_of(h, idx)) : 1u, p);
+                        if (!isfinite(z)) bad = 1;
+                        ok = isfinite(z) && z > tau && z >= bnd;
+                        if (isfinite(z)) pz = fmaxf(pz, z);
+                        x[k][j] = z;
+                      } else {
+                        ok = false;
+                      }
+                    } else {
+                      const float z = xv / p.T;
+                      pz = fmaxf(pz, z);
+                      x[k][j] = z;
+                    }
+                  }
+                }
+                bal[e] = __ballot(ok);
+              }
+            }
+          }
+          wm = uni(fmaxf(wm, wave_max_dpp(pz)));
+        }
+        uint32_t wn = 0;
+#pragma unroll
+        for (int e = 0; e < NE - 1; ++e) wn += (uint32_t)__popcll(bal[e]);
         const uint64_t kg = ckey(zg, tg);
         bal[NE - 1] = __ballot(zg > NEG_INF && kg > tk && zg >= bnd);
         wn += (uint32_t)__popcll(bal[NE - 1]);
@@ -1384,8 +1459,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
                 const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[e] >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal[e], 0u));
                 const uint64_t key =
-                    e == NE - 1 ? kg
-                                : ckey(xm[e / G][e % G] / p.T, (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
+                    e == NE - 1 ? kg : ckey(x[e / G][e % G], (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
                 cand[pos + below] = key;
               }
               pos += (int)__popcll(bal[e]);
@@ -1393,14 +1467,15 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
           }
           count += total;
         } else {
-          // the batch does not fit: one round per tile, then the history round
+          // the batch does not fit: one round per tile, then the history round; each
+          // round tests the passers' z against the compacted buffer's tau
 #pragma unroll
           for (int k = 0; k < PF; ++k) {
-            const float th2 = x_threshold(tau, bnd, p);
+            const float tau2 = tau;
             const int base = (t0 + k) * TILE + tid * G;
             round([&](int j, uint64_t& key) {
-                    key = ckey(xm[k][j] / p.T, (uint32_t)(base + j));
-                    return xm[k][j] >= th2;
+                    key = ckey(x[k][j], (uint32_t)(base + j));
+                    return ((bal[k * G + j] >> lane) & 1ull) && x[k][j] > tau2 && x[k][j] >= bnd;
                   }, G);
           }
           const uint64_t tk2 = tau_key;
@@ -1420,7 +1495,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
             z2 = pen_z(load_one<TIn>(rs, (int)t2), count_of(h, s), p);
             if (!isfinite(z2)) bad = 1;
           }
-          wm = fmaxf(wm, wave_max_dpp(z2));
+          wm = uni(fmaxf(wm, wave_max_dpp(z2)));
           const float bnd2 = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
           const uint64_t k2 = ckey(z2, t2), tk3 = tau_key;
           round([&](int, uint64_t& key) {
@@ -1429,16 +1504,19 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
                 }, 1);
         }
       });
-  // raw non-finite logits make z non-finite (penalties keep infinities and NaN)
-  if (nfx) bad = 1;
-  // a finite x can still overflow x / T; rare, so such rows re-check every element
+  // NaN and +inf logits passed the filter and flagged the row there; -inf, and a finite
+  // x whose x / T or penalized value could overflow, show in |x|: rare, so such rows
+  // re-check every element
   const float axw = wave_max_dpp(ax);
-  if (!isfinite(axw / p.T)) atomicOr(&m->status, 16);
+  const float pen_mag = p.has_pen ? axw * fmaxf(1.0f, p.rp) + fabsf(p.pres) + fabsf(p.freq) * (float)p.hstride : 0.0f;
+  if (!isfinite(axw / p.T) || !isfinite(pen_mag / p.T)) atomicOr(&m->status, 16);
   __syncthreads();
   if (m->status & 16) {
     for (int i = tid; i < p.V; i += NT) {
       const bool pen = p.has_pen && ((h.bitmap[i >> 5] >> (i & 31)) & 1u);
-      if (!pen && !isfinite(load_one<TIn>(rs, i) / p.T)) bad = 1;
+      const float xi = load_one<TIn>(rs, i);
+      const float z = pen ? pen_z(xi, U > 0 ? count_of(h, slot_of(h, i)) : 1u, p) : xi / p.T;
+      if (!isfinite(z)) bad = 1;
     }
     __syncthreads();
     if (tid == 0) m->status &= ~16;
@@ -1546,12 +1624,13 @@ __global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
   constexpr int TILE = NT * G;
   int bad = 0;
   int U = 0;
-  stream_row<TIn, G, NT, VEC>(
+  stream_row<TIn, G, NT, VEC, false>(
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
         __syncthreads();
         if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
       [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
@@ -1803,6 +1882,8 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   p.top_k = d->top_k;
   p.greedy = d->greedy ? 1 : 0;
   p.has_pen = pl.has_pen ? 1 : 0;
+  p.pen_lowers = pl.has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&
+                 d->frequency_penalty >= 0.0f ? 1 : 0;
   // z = x / T by the three-operation scheme needs x / T normal and finite for
   // 2^-100 <= |x| < 2^100, which holds for T in [2^-20, 2^20]; other temperatures
   // take IEEE division for every element.
