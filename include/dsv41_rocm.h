@@ -331,7 +331,11 @@ size_t dsv41_logprob_shard_desc_size(void);
 size_t dsv41_logprob_combine_desc_size(void);
 const char* dsv41_last_error(void);
 
-/* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch. */
+/* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch.
+ * Workspace (8-byte aligned, contents need no initialisation): rows*vocab*4 bytes for
+ * top-p / min-p without top-k (the radix path); rows*(256*8+4) bytes for top-k batches
+ * above 256 rows, whose rows hand up to 256 candidate keys and a count to a second
+ * kernel on the same stream for the final selection; none otherwise. */
 size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* desc);
 int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream /* hipStream_t */);

@@ -91,13 +91,20 @@ def test_sampler_rejects_bad_descriptors_before_launch(kw, code, msg):
     assert msg in _lib.last_error()
 
 
-def test_sampler_workspace_only_for_the_radix_path():
+def test_sampler_workspace_for_the_radix_path_and_deferred_selection():
     lib = _lib.load()
     assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc())) == 0
     assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(top_k=5))) == 0
     assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(top_p=0.9))) == 4 * 100 * 4
     d = _sampler_desc(top_p=0.9)
     assert lib.dsv41_sampler_run(ctypes.byref(d), None, 0, None) == _lib.E_WORKSPACE
+    # top-k batches above 256 rows hand each row's candidates (up to 256 keys and a count) to a
+    # second kernel; small batches and the full-vocabulary path need nothing
+    big = _sampler_desc(top_k=5, rows=300)
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(big)) == 300 * (256 * 8 + 4)
+    assert lib.dsv41_sampler_run(ctypes.byref(big), None, 0, None) == _lib.E_WORKSPACE
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(top_k=5, rows=256))) == 0
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(rows=300))) == 0
 
 
 def _logprob_desc(**kw):

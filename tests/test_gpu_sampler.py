@@ -76,8 +76,29 @@ def test_config_b_greedy_is_first_argmax():
 
 
 def test_config_e_reduced_rows():
-    inp = workloads.sampler_inputs("E", rows=256)
+    # above 256 rows the final selection runs in its own kernel
+    inp = workloads.sampler_inputs("E", rows=320)
     gpu, ora = run_both(inp["logits"], inp["uniforms"], inp["history"], **inp["knobs"])
+    assert_exact(gpu, ora)
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_deferred_selection_mixed_rows(greedy):
+    """A top-k batch above 256 rows: rows whose candidates fit one wave are finished by the
+    second kernel, flat rows (more than 256 candidates) in place, and the statuses of a
+    non-finite row and a bad uniform survive the hand-over."""
+    g = torch.Generator().manual_seed(21)
+    rows, V = 300, 5003
+    logits = 3.0 * torch.randn(rows, V, generator=g)
+    logits[::5] = 0.01 * torch.randn(rows // 5 + (rows % 5 > 0), V, generator=g)  # flat: many candidates
+    logits[7, 123] = float("nan")
+    u = torch.rand(rows, generator=g)
+    u[11] = 1.0  # outside [0, 1)
+    hist = torch.randint(0, V, (rows, 64), generator=g)
+    knobs = dict(top_k=300, top_p=0.95, repetition_penalty=1.1)
+    gpu, ora = run_both(logits, None if greedy else u, hist, greedy=greedy, **knobs)
+    np.testing.assert_array_equal(gpu[3], ora[3])
+    assert gpu[3][7] & 1 and (greedy or gpu[3][11] & 4)
     assert_exact(gpu, ora)
 
 

@@ -46,6 +46,9 @@ constexpr int TOPK_TILE = TOPK_NT * TOPK_G;    // 2048
 constexpr int KCAP = TOPK_TILE;                // largest top_k on the one-pass path
 constexpr int MAX_VOCAB = 1 << 21;             // 2^21 * 2^43 < 2^64: mass sums cannot wrap
 constexpr int MAX_UNIQUE = 65535;              // history slots and counts are 16-bit
+constexpr int DEFER_KEYS = 4 * 64;             // candidates a one-wave final selection holds
+constexpr int DEFER_MIN_ROWS = 256;            // batches above one row per CU defer it
+constexpr int SEL_WAVES = 4;                   // rows per select_kernel workgroup
 constexpr size_t LDS_LIMIT = 160 * 1024;
 
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -77,6 +80,11 @@ struct Params {
   float T, rT, rp, pres, freq, top_p, min_p, lmin_f;
   int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words, cap;
   int pen_lowers;  // penalties can only lower a logit: rp >= 1, presence >= 0, frequency >= 0
+  // TOPK rows whose candidates fit one wave leave them here for select_kernel:
+  // defer_keys[row * DEFER_KEYS + i], defer_count[row] (0: the row was finished in place)
+  uint64_t* defer_keys;
+  int32_t* defer_count;
+  int defer;
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -1526,6 +1534,18 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
 
   // final selection over the candidates: one wave when they fit its registers
   const int n = count;
+  if (p.defer && n >= 1 && n <= DEFER_KEYS) {
+    // The selection is a serial chain of about 15k cycles in one wave; select_kernel
+    // runs it for all rows at once, so this workgroup's slot goes back to streaming.
+    uint64_t* dk = p.defer_keys + (int64_t)row * DEFER_KEYS;
+    for (int i = tid; i < n; i += NT) dk[i] = cand[i];
+    if (tid == 0) {
+      p.defer_count[row] = n;
+      p.out_status[row] = m->status;
+    }
+    return;
+  }
+  if (p.defer && tid == 0) p.defer_count[row] = 0;
   if (n >= 1 && n <= 4 * 64) {
     if (wid == 0) {
       const float u = row_uniform(p, row, m);
@@ -1747,6 +1767,27 @@ __global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
   }
 }
 
+// One wave per deferred TOPK row: the final selection over the row's candidates,
+// exactly as topk_kernel runs it in place.  The row's status so far is in out_status.
+__global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int rows) {
+  __shared__ Misc ms[SEL_WAVES];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int row = blockIdx.x * SEL_WAVES + wid;
+  if (row >= rows) return;
+  const int n = p.defer_count[row];
+  if (n < 1 || n > DEFER_KEYS) return;
+  Misc* m = &ms[wid];
+  if (lane == 0) m->status = p.out_status[row];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float u = row_uniform(p, row, m);
+  const uint64_t* keys = p.defer_keys + (int64_t)row * DEFER_KEYS;
+  if (n <= 64) wave_final<1>(p, row, m, keys, n, u);
+  else if (n <= 128) wave_final<2>(p, row, m, keys, n, u);
+  else wave_final<4>(p, row, m, keys, n, u);
+}
+
 // ====================================================================== host
 template <class K>
 int launch(K kernel, int nt, size_t lds, int rows, const Params& prm, hipStream_t stream) {
@@ -1762,6 +1803,7 @@ struct Plan {
   int esize;
   bool vec;
   bool has_pen;
+  bool defer;
   int words, ucap, cap;
   size_t lds;
   size_t workspace;
@@ -1826,7 +1868,10 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
   pl->lds = L.total;
   if (pl->lds > LDS_LIMIT)
     return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
-  pl->workspace = pl->mode == MODE_GENERIC ? (size_t)d->rows * (size_t)V * sizeof(float) : 0;
+  pl->defer = pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
+  if (pl->mode == MODE_GENERIC) pl->workspace = (size_t)d->rows * (size_t)V * sizeof(float);
+  else if (pl->defer) pl->workspace = (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
+  else pl->workspace = 0;
   return DSV41_OK;
 }
 
@@ -1892,6 +1937,12 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   p.ucap = pl.ucap;
   p.words = pl.words;
   p.cap = pl.cap;
+  if (pl.defer) {
+    p.defer = 1;
+    p.defer_keys = static_cast<uint64_t*>(workspace);
+    p.defer_count = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                               (size_t)d->rows * DEFER_KEYS * sizeof(uint64_t));
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = pl.esize == 2;
   switch (pl.mode) {
@@ -1906,11 +1957,17 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
                             : launch(full_kernel<uint16_t, 8, false, false>, FULL_NT, pl.lds, d->rows, p, s);
       return pl.vec ? launch(full_kernel<float, 4, true, false>, FULL_NT, pl.lds, d->rows, p, s)
                     : launch(full_kernel<float, 4, false, false>, FULL_NT, pl.lds, d->rows, p, s);
-    case MODE_TOPK:
-      if (bf) return pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
-                            : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
-                    : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
+    case MODE_TOPK: {
+      if (bf) rc = pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
+                          : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
+      else rc = pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
+                       : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
+      if (rc != DSV41_OK || !pl.defer) return rc;
+      hipLaunchKernelGGL(select_kernel, dim3((d->rows + SEL_WAVES - 1) / SEL_WAVES), dim3(SEL_WAVES * 64), 0, s,
+                         p, d->rows);
+      DSV41_HIP_CHECK(hipGetLastError());
+      return DSV41_OK;
+    }
     default:
       if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
                             : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, pl.lds, d->rows, p, s);
