@@ -18,6 +18,8 @@
  *   dsv41_logprob_run  <- dsv41_train/models/dsv4/model.py:679-684 (_token_log_probs),
  *                         dsv41_train/rl/native_lora.py:80-82 (_score_targets),
  *                         plus the Token-TIS weight of dsv41_train/rl/algorithm.py:293-299.
+ *   dsv41_sampler_shard_run + dsv41_sampler_merge_run <- the same lines for logits whose
+ *                         vocabulary is split over tensor-parallel GPUs.
  *   dsv41_grpo_run     <- dsv41_train/rl/algorithm.py:169-246 (grpo_loss).
  *   dsv41_token_tis_run <- dsv41_train/rl/algorithm.py:249-346 (decoupled_token_tis_loss)
  *                         with the metric pooling of dsv41_train/rl/distributed_grpo.py:197-222.
@@ -103,6 +105,51 @@ typedef struct dsv41_sampler_desc {
   const float* exponentials;       /* [rows, exponentials_row_stride] or NULL */
   int64_t exponentials_row_stride; /* in elements, >= vocab */
 } dsv41_sampler_desc;
+
+/*
+ * One GPU's slice of vocabulary-sharded logits (a tensor-parallel head): `sampler` describes
+ * the slice [rows, vocab] holding the ids [vocab_offset, vocab_offset + vocab) of a vocab_size
+ * vocabulary, with the row knobs of the whole batch (1 <= top_k <= 2048).
+ * History ids are global; sampler->uniforms, out_ids, out_logprob and out_kept are unused.
+ * For each row the slice emits its exact local top_k under the local min-p bound: at most
+ * top_k candidate keys, each
+ *   key = (okey(z) << 32) | (0xFFFFFFFF - global id),
+ *   okey(z) = bits(z) | 0x80000000 for z >= 0, ~bits(z) for z < 0 (-0 as +0),
+ * so that keys order as (z descending, id ascending).  The row's local maximum is at most
+ * its global one, so the union of the slices' lists holds the row's kept set, and
+ * dsv41_sampler_merge_run finishes every row exactly as dsv41_sampler_run would.  The lists
+ * (up to 8 * top_k bytes per row and slice), counts and status bits are the wire format.
+ */
+typedef struct dsv41_sampler_shard_desc {
+  uint32_t struct_size;              /* = sizeof(dsv41_sampler_shard_desc) */
+  int32_t max_candidates;            /* keys per row in out_keys, >= sampler->top_k */
+  const dsv41_sampler_desc* sampler;
+  int64_t vocab_offset;              /* global id of the slice's first column */
+  int64_t vocab_size;                /* the whole vocabulary; larger history ids flag the row */
+  uint64_t* out_keys;                /* [rows, max_candidates] */
+  int32_t* out_counts;               /* [rows] */
+  int32_t* out_status;               /* [rows] DSV41_STATUS_* bits seen by this slice */
+} dsv41_sampler_shard_desc;
+
+/* Finishes a sharded batch from the gathered lists of all slices. */
+typedef struct dsv41_sampler_merge_desc {
+  uint32_t struct_size;    /* = sizeof(dsv41_sampler_merge_desc) */
+  int32_t rows;
+  int32_t n_shards;
+  int32_t max_candidates;  /* keys per row and slice in `keys` */
+  const uint64_t* keys;    /* [n_shards, rows, max_candidates] */
+  const int32_t* counts;   /* [n_shards, rows] */
+  const int32_t* status;   /* [n_shards, rows] */
+  const float* uniforms;   /* [rows]; may be NULL only when greedy != 0 */
+  int32_t top_k;           /* the knobs of the shard launches */
+  float top_p;
+  float min_p;
+  int32_t greedy;
+  int64_t* out_ids;        /* [rows] */
+  float* out_logprob;      /* [rows] */
+  int32_t* out_kept;       /* [rows] or NULL */
+  int32_t* out_status;     /* [rows]: the OR of the slices' bits and the uniform check */
+} dsv41_sampler_merge_desc;
 
 /*
  * Fused selected-token log-prob.  logits = x[N,H] @ w[V,H]^T in fp32 (never stored),
@@ -329,6 +376,8 @@ size_t dsv41_token_tis_desc_size(void);
 size_t dsv41_grpo_desc_size(void);
 size_t dsv41_logprob_shard_desc_size(void);
 size_t dsv41_logprob_combine_desc_size(void);
+size_t dsv41_sampler_shard_desc_size(void);
+size_t dsv41_sampler_merge_desc_size(void);
 const char* dsv41_last_error(void);
 
 /* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch.
@@ -339,6 +388,12 @@ const char* dsv41_last_error(void);
 size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* desc);
 int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream /* hipStream_t */);
+
+/* Vocabulary-sharded sampler: per-slice candidate lists, then the exact merge (no workspace).
+ * Together they replace rollout.py:144-150 when the head's vocabulary is split over GPUs;
+ * the lists are what one all-gather would carry between the two calls. */
+int dsv41_sampler_shard_run(const dsv41_sampler_shard_desc* desc, void* stream /* hipStream_t */);
+int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* desc, void* stream /* hipStream_t */);
 
 /* Fused selected-token log-prob: replaces model.py:679-684 / native_lora.py:80-82. */
 size_t dsv41_logprob_workspace_bytes(const dsv41_logprob_desc* desc);

@@ -36,7 +36,8 @@ def test_descriptor_layouts_match_header(tmp_path):
     fields = {"dsv41_sampler_desc": _lib.SamplerDesc, "dsv41_logprob_desc": _lib.LogprobDesc,
               "dsv41_logprob_grad_desc": _lib.LogprobGradDesc, "dsv41_token_tis_desc": _lib.TokenTisDesc,
               "dsv41_grpo_desc": _lib.GrpoDesc,
-              "dsv41_logprob_shard_desc": _lib.LogprobShardDesc, "dsv41_logprob_combine_desc": _lib.LogprobCombineDesc}
+              "dsv41_logprob_shard_desc": _lib.LogprobShardDesc, "dsv41_logprob_combine_desc": _lib.LogprobCombineDesc,
+              "dsv41_sampler_shard_desc": _lib.SamplerShardDesc, "dsv41_sampler_merge_desc": _lib.SamplerMergeDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {", 'printf("{");']
     first = True
     for cname, cls in fields.items():
@@ -214,3 +215,60 @@ def test_custom_ops_have_no_cpu_kernel():
     with pytest.raises(NotImplementedError):
         torch.ops.dsv41_rocm.sample_rows(torch.zeros(2, 10), torch.rand(2), None, None,
                                          1.0, 1.0, 0.0, 0.0, 0, 1.0, 0.0, False)
+
+
+def _shard_desc(sampler, **kw):
+    d = _lib.SamplerShardDesc()
+    d.struct_size = ctypes.sizeof(_lib.SamplerShardDesc)
+    d.max_candidates = 5
+    d.sampler = ctypes.pointer(sampler)
+    d.vocab_offset, d.vocab_size = 100, 400
+    d.out_keys, d.out_counts, d.out_status = 0x7000, 0x8000, 0x9000
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("skw,kw,code,msg", [
+    (dict(top_k=0), {}, _lib.E_UNSUPPORTED, "needs 1 <= top_k <= 2048"),
+    (dict(top_k=3000), dict(max_candidates=3000), _lib.E_UNSUPPORTED, "needs 1 <= top_k <= 2048"),
+    (dict(top_k=5, top_p=0.9, min_p=0.0), dict(max_candidates=4), _lib.E_INVALID, "max_candidates"),
+    (dict(top_k=5), dict(vocab_offset=350), _lib.E_INVALID, "within a vocabulary"),
+    (dict(top_k=5), dict(out_keys=None), _lib.E_INVALID, "out_keys"),
+    (dict(top_k=5, exponentials=0x6000, exponentials_row_stride=100), {}, _lib.E_UNSUPPORTED, "exponential"),
+    (dict(top_k=5), dict(struct_size=8), _lib.E_ABI, "size mismatch"),
+])
+def test_sampler_shard_rejects_bad_descriptors(skw, kw, code, msg):
+    lib = _lib.load()
+    base = _sampler_desc(uniforms=None, out_ids=None, out_logprob=None, **skw)  # a slice needs neither
+    d = _shard_desc(base, **kw)
+    assert lib.dsv41_sampler_shard_run(ctypes.byref(d), None) == code
+    assert msg in _lib.last_error()
+
+
+def _merge_desc(**kw):
+    d = _lib.SamplerMergeDesc()
+    d.struct_size = ctypes.sizeof(_lib.SamplerMergeDesc)
+    d.rows, d.n_shards, d.max_candidates = 4, 8, 64
+    d.keys, d.counts, d.status, d.uniforms = 0x1000, 0x2000, 0x3000, 0x4000
+    d.top_k, d.top_p, d.min_p = 64, 1.0, 0.0
+    d.out_ids, d.out_logprob, d.out_status = 0x5000, 0x6000, 0x7000
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(rows=0), _lib.E_INVALID, "must be positive"),
+    (dict(top_k=0), _lib.E_INVALID, "top_k must be in [1, 2048]"),
+    (dict(top_p=1.5), _lib.E_INVALID, "top_p"),
+    (dict(uniforms=None), _lib.E_INVALID, "uniform"),
+    (dict(keys=None), _lib.E_INVALID, "keys, counts"),
+    (dict(n_shards=64, max_candidates=2048, top_k=2048), _lib.E_UNSUPPORTED, "candidate buffer"),
+    (dict(struct_size=8), _lib.E_ABI, "size mismatch"),
+])
+def test_sampler_merge_rejects_bad_descriptors(kw, code, msg):
+    lib = _lib.load()
+    d = _merge_desc(**kw)
+    assert lib.dsv41_sampler_merge_run(ctypes.byref(d), None) == code
+    assert msg in _lib.last_error()

@@ -1,0 +1,115 @@
+"""GPU parity of vocabulary-sharded sampling: the logits of a batch split into slices of a
+tensor-parallel head, each slice's candidate list (dsv41_sampler_shard_run), then the exact
+merge (dsv41_sampler_merge_run), all on one GPU.  The merged ids, kept sets and statuses
+must equal the unsharded sampler's and the C oracle's; log-probs agree within 1e-6 with the
+unsharded sampler (the kept-set sum may run in another order) and 1e-4 with the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dsv41_rocm import merge_shards, sample, sample_shard, workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def edges(vocab, n, seed):
+    """n ragged slices covering [0, vocab)."""
+    g = torch.Generator().manual_seed(seed)
+    cuts = sorted(torch.randperm(vocab - 1, generator=g)[: n - 1].add(1).tolist())
+    return [0] + cuts + [vocab]
+
+
+def run_sharded(logits, bounds, uniforms=None, history=None, greedy=False, **knobs):
+    sk = {k: v for k, v in knobs.items() if k != "greedy"}
+    shards = []
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        print(f"case: slice [{a}, {b}) of {logits.shape[1]} knobs={knobs}", flush=True)
+        shards.append(sample_shard(logits[:, a:b], vocab_offset=a, vocab_size=logits.shape[1],
+                                   history=history, **sk))
+    merged = merge_shards(shards, top_k=knobs["top_k"], top_p=knobs.get("top_p", 1.0),
+                          min_p=knobs.get("min_p", 0.0), uniforms=uniforms, greedy=greedy, check=False)
+    torch.cuda.synchronize()
+    return merged, shards
+
+
+def assert_same(merged, whole, ora=None):
+    for name in ("ids", "kept", "status"):
+        assert torch.equal(getattr(merged, name), getattr(whole, name)), name
+    ok = (whole.status == 0)
+    diff = (merged.logprobs - whole.logprobs)[ok].abs()
+    assert diff.numel() == 0 or float(diff.max()) <= 1e-6
+    if ora is not None:
+        oids, olp, okept, ost = ora
+        np.testing.assert_array_equal(merged.status.cpu().numpy(), ost)
+        okr = ost == 0
+        np.testing.assert_array_equal(merged.ids.cpu().numpy()[okr], oids[okr])
+        np.testing.assert_array_equal(merged.kept.cpu().numpy()[okr], okept[okr])
+        assert np.max(np.abs(merged.logprobs.cpu().numpy()[okr] - olp[okr]), initial=0.0) <= 1e-4
+
+
+@pytest.mark.parametrize("n_shards", [2, 8])
+def test_config_e_split_over_slices(n_shards):
+    inp = workloads.sampler_inputs("E", rows=96, device=DEV)
+    x, u, h, knobs = inp["logits"], inp["uniforms"], inp["history"], inp["knobs"]
+    bounds = edges(x.shape[1], n_shards, seed=n_shards)
+    merged, shards = run_sharded(x, bounds, uniforms=u, history=h, **knobs)
+    whole = sample(x, uniforms=u, history=h, check=False, **knobs)
+    ora = oracle.sample(x.float().cpu().numpy(), uniforms=u.cpu().numpy(), history=h.cpu().numpy(), **knobs)
+    assert_same(merged, whole, ora)
+    # what crosses the wire: at most top_k keys per row and slice, typically a few dozen
+    assert all(int(s.counts.max()) <= knobs["top_k"] for s in shards)
+
+
+@pytest.mark.parametrize("knobs", [
+    dict(temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.3),                # lowering, bitmap only
+    dict(temperature=1.1, top_k=200, min_p=0.02, presence_penalty=0.5, frequency_penalty=0.2),  # with counts
+    dict(temperature=0.8, top_k=30, repetition_penalty=0.8, presence_penalty=-0.3),    # raising: gathered
+    dict(temperature=0.9, top_k=1),
+    dict(temperature=0.6, top_k=50, greedy=True),
+])
+def test_knobs_and_penalties_across_slices(knobs):
+    g = torch.Generator().manual_seed(17)
+    rows, V = 40, 20011
+    x = (2.0 * torch.randn(rows, V, generator=g)).to(DEV)
+    u = torch.rand(rows, generator=g).to(DEV)
+    h = torch.randint(-1, V, (rows, 500), generator=g).to(DEV)
+    bounds = edges(V, 5, seed=3)
+    greedy = knobs.get("greedy", False)
+    merged, _ = run_sharded(x, bounds, uniforms=None if greedy else u, history=h, **knobs)
+    whole = sample(x, uniforms=None if greedy else u, history=h, check=False, **knobs)
+    ora = oracle.sample(x.cpu().numpy(), uniforms=None if greedy else u.cpu().numpy(), history=h.cpu().numpy(),
+                        **knobs)
+    assert_same(merged, whole, ora)
+
+
+def test_bf16_flat_rows_statuses_and_the_block_merge():
+    """bf16 slices; flat rows whose merged lists exceed one wave (the block merge); a NaN in
+    one slice, an id past the vocabulary and a bad uniform flag their rows as unsharded."""
+    g = torch.Generator().manual_seed(29)
+    rows, V = 24, 30000
+    x = 3.0 * torch.randn(rows, V, generator=g)
+    x[::3] = 0.001 * torch.randn((rows + 2) // 3, V, generator=g)
+    x[4, 12345] = float("nan")
+    x = x.to(torch.bfloat16).to(DEV)
+    u = torch.rand(rows, generator=g)
+    u[5] = 1.5
+    u = u.to(DEV)
+    h = torch.randint(0, V, (rows, 64), generator=g)
+    h[6, 3] = V + 7
+    h = h.to(DEV)
+    knobs = dict(temperature=0.9, top_k=400, top_p=0.95, repetition_penalty=1.1)
+    bounds = edges(V, 6, seed=5)
+    bounds = sorted(set(bounds + [bounds[1] + 100]))  # one slice narrower than top_k
+    merged, shards = run_sharded(x, bounds, uniforms=u, history=h, **knobs)
+    whole = sample(x, uniforms=u, history=h, check=False, **knobs)
+    assert_same(merged, whole)
+    st = merged.status.cpu().tolist()
+    assert st[4] & 1 and st[5] & 4 and st[6] & 2
+    assert int(sum(s.counts for s in shards)[0]) > 256  # row 0 is flat: the block path merged it
+    with pytest.raises(ValueError, match="non-finite"):
+        merge_shards(shards, top_k=400, top_p=0.95, uniforms=u)

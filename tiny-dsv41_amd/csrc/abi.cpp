@@ -20,4 +20,6 @@ extern "C" size_t dsv41_token_tis_desc_size(void) { return sizeof(dsv41_token_ti
 extern "C" size_t dsv41_grpo_desc_size(void) { return sizeof(dsv41_grpo_desc); }
 extern "C" size_t dsv41_logprob_shard_desc_size(void) { return sizeof(dsv41_logprob_shard_desc); }
 extern "C" size_t dsv41_logprob_combine_desc_size(void) { return sizeof(dsv41_logprob_combine_desc); }
+extern "C" size_t dsv41_sampler_shard_desc_size(void) { return sizeof(dsv41_sampler_shard_desc); }
+extern "C" size_t dsv41_sampler_merge_desc_size(void) { return sizeof(dsv41_sampler_merge_desc); }
 extern "C" const char* dsv41_last_error(void) { return dsv41::g_last_error.c_str(); }

@@ -85,6 +85,11 @@ struct Params {
   uint64_t* defer_keys;
   int32_t* defer_count;
   int defer;
+  // vocabulary shard (topk_kernel<..., EMIT>): this launch sees ids [voff, voff + V) of a
+  // vocab_size = vfull vocabulary and emits each row's candidates instead of sampling
+  int voff, vfull, emit_cap;
+  uint64_t* emit_keys;  // [rows, emit_cap]
+  int32_t* emit_count;  // [rows]
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -480,9 +485,11 @@ __device__ __forceinline__ void load_history(const Params& p, int row, HistIds<H
 
 // Builds the tables; returns the number of slots (distinct in-vocabulary ids).  With
 // counts false only the membership bitmap is built and 0 is returned.
-template <int NT, int HR>
+template <int NT, int HR, bool SHARD = false>
 __device__ __forceinline__ int build_history(const Params& p, int row, const HistIds<HR>& hi, const Hist& h, Misc* m,
                                              bool counts = true) {
+  // a vocabulary shard keeps the ids of its own range; ids past the whole vocabulary flag the row
+  const int64_t id_off = SHARD ? p.voff : 0, id_lim = SHARD ? p.vfull : p.V;
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int W = p.words;
@@ -496,15 +503,15 @@ __device__ __forceinline__ int build_history(const Params& p, int row, const His
   for (int j = 0; j < HR; ++j) {
     const int idx = tid + j * NT;
     if (idx < hl) {
-      const int64_t id = hi.id[j];
+      const int64_t g = hi.id[j], id = g - id_off;
       if (id >= 0 && id < p.V) atomicOr(&h.bitmap[id >> 5], 1u << (id & 31));
-      else if (id >= p.V) bad = 1;
+      else if (g >= id_lim) bad = 1;
     }
   }
   for (int idx = tid + HR * NT; idx < hl; idx += NT) {
-    const int64_t id = hr[idx];
+    const int64_t g = hr[idx], id = g - id_off;
     if (id >= 0 && id < p.V) atomicOr(&h.bitmap[id >> 5], 1u << (id & 31));
-    else if (id >= p.V) bad = 1;
+    else if (g >= id_lim) bad = 1;
   }
   if (bad) atomicOr(&m->status, ST_BAD_HISTORY);
   __syncthreads();
@@ -526,7 +533,8 @@ __device__ __forceinline__ int build_history(const Params& p, int row, const His
   int U = 0;
   for (int i = 0; i < NW; ++i) U += m->ri[i];
   __syncthreads();
-  auto count_id = [&](int64_t id) {
+  auto count_id = [&](int64_t g) {
+    const int64_t id = g - id_off;
     if (id >= 0 && id < p.V) {
       const int slot = slot_of(h, (int)id);
       atomicAdd(&h.cnt2[slot >> 1], 1u << ((slot & 1) * 16));
@@ -1254,7 +1262,87 @@ __device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, co
   }
 }
 
-template <typename TIn, bool VEC>
+// Final selection over the n candidate keys in cand by the whole workgroup: bitonic sort,
+// then exact scans for min-p, top-k and top-p, and the draw by radix selection.  cand
+// holds max(n, 2 * min(top_k, n)) keys (the masses reuse the space past the top-k);
+// hist is 256 keys of scratch.
+template <int NT>
+__device__ __forceinline__ void block_final(const Params& p, int row, Misc* m, uint64_t* cand, int n,
+                                            uint64_t* hist) {
+  const int tid = threadIdx.x;
+  bitonic_sort_desc<NT>(cand, n);
+  const float u = row_uniform(p, row, m);
+  if (n == 0) {  // only possible for rows without a finite maximum
+    __syncthreads();
+    if (tid == 0) {
+      m->status |= ST_NONFINITE;
+      write_result(p, row, m, -1, 0.0f, 0);
+    }
+    return;
+  }
+  const float zmax = ckey_z(cand[0]);
+  int el = 0;
+  for (int i = tid; i < n; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
+  el = block_sum_i<NT>(el, m);
+  const int K = min(p.top_k, el);
+  uint64_t* q = cand + K;  // the keys past the top-k are not needed again
+  for (int i = tid; i < K; i += NT) q[i] = mass_of(ckey_z(cand[i]), zmax);
+  __syncthreads();
+  int n_keep = K;
+  uint64_t S;
+  if (p.top_p < 1.0f) {
+    block_incl_scan_u64<NT>(q, K, m);
+    const uint64_t thr = top_p_threshold(p.top_p, q[K - 1]);
+    if (tid == 0) m->bi[1] = K - 1;
+    __syncthreads();
+    for (int i = tid; i < K; i += NT)
+      if (q[i] >= thr && (i == 0 || q[i - 1] < thr)) m->bi[1] = i;
+    __syncthreads();
+    n_keep = m->bi[1] + 1;
+    S = q[n_keep - 1];
+    __syncthreads();
+  } else {
+    uint64_t s = 0;
+    for (int i = tid; i < K; i += NT) s += q[i];
+    S = block_sum_u64<NT>(s, m);
+  }
+  double es = 0.0;
+  for (int i = tid; i < n_keep; i += NT) es += exp_det((double)ckey_z(cand[i]) - (double)zmax);
+  const double esum = block_sum_d<NT>(es, m);
+
+  int64_t tok;
+  float ztok;
+  if (p.greedy) {
+    tok = ckey_idx(cand[0]);
+    ztok = zmax;
+  } else {
+    const uint64_t t = draw_target(u, S);
+    bool found = false;
+    const uint64_t idx = radix_select<NT, false, 24>(
+        [&](auto&& f) {
+          for (int i = tid; i < n_keep; i += NT) {
+            const uint64_t k = cand[i];
+            f((uint64_t)ckey_idx(k), mass_of(ckey_z(k), zmax));
+          }
+        },
+        t + 1, hist, m, &found);
+    tok = found ? (int64_t)idx : (int64_t)ckey_idx(cand[0]);
+    if (tid == 0) m->bf[0] = zmax;
+    __syncthreads();
+    for (int i = tid; i < n_keep; i += NT)
+      if (ckey_idx(cand[i]) == (uint32_t)tok) m->bf[0] = ckey_z(cand[i]);
+    __syncthreads();
+    ztok = m->bf[0];
+  }
+  if (tid == 0) {
+    const float lp = (float)(((double)ztok - (double)zmax) - log(esum));
+    write_result(p, row, m, tok, lp, n_keep);
+  }
+}
+
+// EMIT: the launch covers one vocabulary shard; each row's candidates leave for
+// merge_kernel instead of being sampled here.
+template <typename TIn, bool VEC, bool EMIT = false>
 __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   constexpr int NT = TOPK_NT, NW = NT / 64, G = TOPK_G, TILE = TOPK_TILE, HR = 8;
   constexpr int NE = PF * G + 1;  // elements per thread in one batch round (+1 history slot)
@@ -1344,7 +1432,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
         __syncthreads();
         // with lowering penalties the stream evaluates history tokens itself and needs
         // their counts only for a frequency penalty
-        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m, !p.pen_lowers || p.freq != 0.0f);
+        if (p.has_pen) U = build_history<NT, HR, EMIT>(p, row, hi, h, m, !p.pen_lowers || p.freq != 0.0f);
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
@@ -1532,6 +1620,30 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
 
+  if constexpr (EMIT) {
+    // Vocabulary shard: the exact local top_k under the local min-p bound.  The local
+    // maximum is at most the row's, so every token of the row's kept set is in its
+    // shard's list, and merge_kernel finishes the row from the union of the lists.
+    int keep = 0;
+    if (count > 0) {
+      bitonic_sort_desc<NT>(cand, count);
+      const float zmax = ckey_z(cand[0]);
+      int el = 0;
+      for (int i = tid; i < count; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
+      keep = min(p.top_k, block_sum_i<NT>(el, m));
+    }
+    uint64_t* out = p.emit_keys + (int64_t)row * p.emit_cap;
+    for (int i = tid; i < keep; i += NT) {
+      const uint64_t k = cand[i];
+      out[i] = ckey(ckey_z(k), ckey_idx(k) + (uint32_t)p.voff);
+    }
+    if (tid == 0) {
+      p.emit_count[row] = keep;
+      p.out_status[row] = m->status;
+    }
+    return;
+  }
+
   // final selection over the candidates: one wave when they fit its registers
   const int n = count;
   if (p.defer && n >= 1 && n <= DEFER_KEYS) {
@@ -1555,74 +1667,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
     }
     return;
   }
-  bitonic_sort_desc<NT>(cand, n);
-  const float u = row_uniform(p, row, m);
-  if (n == 0) {  // only possible for rows without a finite maximum
-    __syncthreads();
-    if (tid == 0) {
-      m->status |= ST_NONFINITE;
-      write_result(p, row, m, -1, 0.0f, 0);
-    }
-    return;
-  }
-  const float zmax = ckey_z(cand[0]);
-  int el = 0;
-  for (int i = tid; i < n; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
-  el = block_sum_i<NT>(el, m);
-  const int K = min(p.top_k, el);
-  uint64_t* q = cand + K;  // K <= KCAP = TILE and cap = top_k + TILE >= 2K
-  for (int i = tid; i < K; i += NT) q[i] = mass_of(ckey_z(cand[i]), zmax);
-  __syncthreads();
-  int n_keep = K;
-  uint64_t S;
-  if (p.top_p < 1.0f) {
-    block_incl_scan_u64<NT>(q, K, m);
-    const uint64_t thr = top_p_threshold(p.top_p, q[K - 1]);
-    if (tid == 0) m->bi[1] = K - 1;
-    __syncthreads();
-    for (int i = tid; i < K; i += NT)
-      if (q[i] >= thr && (i == 0 || q[i - 1] < thr)) m->bi[1] = i;
-    __syncthreads();
-    n_keep = m->bi[1] + 1;
-    S = q[n_keep - 1];
-    __syncthreads();
-  } else {
-    uint64_t s = 0;
-    for (int i = tid; i < K; i += NT) s += q[i];
-    S = block_sum_u64<NT>(s, m);
-  }
-  double es = 0.0;
-  for (int i = tid; i < n_keep; i += NT) es += exp_det((double)ckey_z(cand[i]) - (double)zmax);
-  const double esum = block_sum_d<NT>(es, m);
-
-  int64_t tok;
-  float ztok;
-  if (p.greedy) {
-    tok = ckey_idx(cand[0]);
-    ztok = zmax;
-  } else {
-    const uint64_t t = draw_target(u, S);
-    bool found = false;
-    const uint64_t idx = radix_select<NT, false, 24>(
-        [&](auto&& f) {
-          for (int i = tid; i < n_keep; i += NT) {
-            const uint64_t k = cand[i];
-            f((uint64_t)ckey_idx(k), mass_of(ckey_z(k), zmax));
-          }
-        },
-        t + 1, hist, m, &found);
-    tok = found ? (int64_t)idx : (int64_t)ckey_idx(cand[0]);
-    if (tid == 0) m->bf[0] = zmax;
-    __syncthreads();
-    for (int i = tid; i < n_keep; i += NT)
-      if (ckey_idx(cand[i]) == (uint32_t)tok) m->bf[0] = ckey_z(cand[i]);
-    __syncthreads();
-    ztok = m->bf[0];
-  }
-  if (tid == 0) {
-    const float lp = (float)(((double)ztok - (double)zmax) - log(esum));
-    write_result(p, row, m, tok, lp, n_keep);
-  }
+  block_final<NT>(p, row, m, cand, n, hist);
 }
 
 // ====================================================================== GENERIC
@@ -1788,6 +1833,55 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int ro
   else wave_final<4>(p, row, m, keys, n, u);
 }
 
+// One workgroup per row of a vocabulary-sharded batch: the final selection over the
+// union of the candidate lists the shards emitted (topk_kernel<..., EMIT>), exactly as an
+// unsharded row would finish.  The row's status is the OR of the shards' statuses.
+struct MergeIn {
+  const uint64_t* keys;   // [shards, rows, stride]
+  const int32_t* counts;  // [shards, rows]
+  const int32_t* status;  // [shards, rows]
+  int shards, rows, stride;
+  int take;  // keys used per list: min(stride, top_k), the size of the LDS buffer's shares
+};
+
+__global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
+  constexpr int NT = TOPK_NT;
+  extern __shared__ __align__(16) unsigned char smem[];
+  Misc* m = reinterpret_cast<Misc*>(smem);
+  uint64_t* hist = reinterpret_cast<uint64_t*>(smem + align16(sizeof(Misc)));
+  uint64_t* cand = hist + 256;
+  const int row = blockIdx.x, tid = threadIdx.x, wid = tid >> 6;
+  if (tid == 0) {
+    int st = 0, n = 0;
+    for (int s = 0; s < in.shards; ++s) {
+      st |= in.status[(int64_t)s * in.rows + row];
+      n += min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
+    }
+    m->status = st;
+    m->count = n;
+  }
+  __syncthreads();
+  const int n = m->count;
+  int base = 0;
+  for (int s = 0; s < in.shards; ++s) {
+    const int c = min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
+    const uint64_t* src = in.keys + ((int64_t)s * in.rows + row) * in.stride;
+    for (int i = tid; i < c; i += NT) cand[base + i] = src[i];
+    base += c;
+  }
+  __syncthreads();
+  if (n >= 1 && n <= 4 * 64) {
+    if (wid == 0) {
+      const float u = row_uniform(p, row, m);
+      if (n <= 64) wave_final<1>(p, row, m, cand, n, u);
+      else if (n <= 128) wave_final<2>(p, row, m, cand, n, u);
+      else wave_final<4>(p, row, m, cand, n, u);
+    }
+    return;
+  }
+  block_final<NT>(p, row, m, cand, n, hist);
+}
+
 // ====================================================================== host
 template <class K>
 int launch(K kernel, int nt, size_t lds, int rows, const Params& prm, hipStream_t stream) {
@@ -1809,7 +1903,9 @@ struct Plan {
   size_t workspace;
 };
 
-int plan(const dsv41_sampler_desc* d, Plan* pl) {
+// shard: the descriptor describes one vocabulary slice (dsv41_sampler_shard_run); the draw
+// and the per-row outputs happen in the merge, so uniforms and outputs are not checked here.
+int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   if (!d) return fail(DSV41_E_INVALID, "sampler descriptor is NULL");
   if (d->struct_size != sizeof(dsv41_sampler_desc))
     return fail(DSV41_E_ABI, "dsv41_sampler_desc size mismatch (rebuild the binding)");
@@ -1829,8 +1925,8 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
   if (d->top_k < 0) return fail(DSV41_E_INVALID, "top_k must be nonnegative");
   if (!(d->top_p > 0.0f && d->top_p <= 1.0f)) return fail(DSV41_E_INVALID, "top_p must be in (0, 1]");
   if (!(d->min_p >= 0.0f && d->min_p <= 1.0f)) return fail(DSV41_E_INVALID, "min_p must be in [0, 1]");
-  if (!d->greedy && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
-  if (!d->out_ids || !d->out_logprob || !d->out_status)
+  if (!shard && !d->greedy && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
+  if (!shard && (!d->out_ids || !d->out_logprob || !d->out_status))
     return fail(DSV41_E_INVALID, "out_ids, out_logprob and out_status are required");
   const bool pen_on = d->repetition_penalty != 1.0f || d->presence_penalty != 0.0f || d->frequency_penalty != 0.0f;
   const bool hist_given = d->history != nullptr && (d->history_lens != nullptr || d->hist_len > 0);
@@ -1849,7 +1945,11 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
     return fail(DSV41_E_UNSUPPORTED, "exponential race draws need the full-vocabulary distribution (no top-k, top-p or min-p)");
   if (d->exponentials && d->exponentials_row_stride < d->vocab)
     return fail(DSV41_E_INVALID, "exponentials row stride must be >= vocab");
-  if (!truncating) pl->mode = MODE_FULL;
+  // a vocabulary slice takes the TOPK kernel for any 1 <= top_k <= 2048: at or above the
+  // slice width its buffer (top_k + 2048 keys) never compacts and it emits every survivor
+  // of the local min-p bound
+  if (shard && d->top_k >= 1 && d->top_k <= KCAP) pl->mode = MODE_TOPK;
+  else if (!truncating) pl->mode = MODE_FULL;
   else if (d->top_k > 0 && d->top_k < V && d->top_k <= KCAP) pl->mode = MODE_TOPK;
   else pl->mode = MODE_GENERIC;
   pl->words = pl->has_pen ? (V + 31) / 32 : 0;
@@ -1868,32 +1968,14 @@ int plan(const dsv41_sampler_desc* d, Plan* pl) {
   pl->lds = L.total;
   if (pl->lds > LDS_LIMIT)
     return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
-  pl->defer = pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
+  pl->defer = !shard && pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
   if (pl->mode == MODE_GENERIC) pl->workspace = (size_t)d->rows * (size_t)V * sizeof(float);
   else if (pl->defer) pl->workspace = (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
   else pl->workspace = 0;
   return DSV41_OK;
 }
 
-}  // namespace sampler
-}  // namespace dsv41
-
-using namespace dsv41;
-using namespace dsv41::sampler;
-
-extern "C" size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* d) {
-  Plan pl;
-  if (plan(d, &pl) != DSV41_OK) return 0;
-  return pl.workspace;
-}
-
-extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
-  Plan pl;
-  int rc = plan(d, &pl);
-  if (rc != DSV41_OK) return rc;
-  if (pl.workspace && (!workspace || workspace_bytes < pl.workspace))
-    return fail(DSV41_E_WORKSPACE, "sampler workspace is missing or too small");
+Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace) {
   Params p{};
   p.logits = d->logits;
   p.lstride = d->logits_row_stride;
@@ -1943,6 +2025,31 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
     p.defer_count = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                                (size_t)d->rows * DEFER_KEYS * sizeof(uint64_t));
   }
+  p.voff = 0;
+  p.vfull = d->vocab;
+  return p;
+}
+
+}  // namespace sampler
+}  // namespace dsv41
+
+using namespace dsv41;
+using namespace dsv41::sampler;
+
+extern "C" size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* d) {
+  Plan pl;
+  if (plan(d, &pl) != DSV41_OK) return 0;
+  return pl.workspace;
+}
+
+extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  Plan pl;
+  int rc = plan(d, &pl);
+  if (rc != DSV41_OK) return rc;
+  if (pl.workspace && (!workspace || workspace_bytes < pl.workspace))
+    return fail(DSV41_E_WORKSPACE, "sampler workspace is missing or too small");
+  Params p = make_params(d, pl, workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = pl.esize == 2;
   switch (pl.mode) {
@@ -1974,4 +2081,72 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
       return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
                     : launch(generic_kernel<float, 4, false>, GEN_NT, pl.lds, d->rows, p, s);
   }
+}
+
+extern "C" int dsv41_sampler_shard_run(const dsv41_sampler_shard_desc* d, void* stream) {
+  if (!d) return fail(DSV41_E_INVALID, "sampler shard descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_sampler_shard_desc))
+    return fail(DSV41_E_ABI, "dsv41_sampler_shard_desc size mismatch (rebuild the binding)");
+  const dsv41_sampler_desc* sd = d->sampler;
+  if (!sd) return fail(DSV41_E_INVALID, "sampler shard: the slice's sampler descriptor is NULL");
+  Plan pl;
+  int rc = plan(sd, &pl, true);
+  if (rc != DSV41_OK) return rc;
+  if (sd->exponentials) return fail(DSV41_E_UNSUPPORTED, "sampler shard: exponential race draws are not sharded");
+  if (pl.mode != MODE_TOPK)
+    return fail(DSV41_E_UNSUPPORTED, "vocabulary-sharded sampling needs 1 <= top_k <= 2048");
+  if (d->vocab_offset < 0 || d->vocab_size < d->vocab_offset + sd->vocab || d->vocab_size > MAX_VOCAB)
+    return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of at most 2^21 ids");
+  if (d->max_candidates < sd->top_k) return fail(DSV41_E_INVALID, "sampler shard: max_candidates must be >= top_k");
+  if (!d->out_keys || !d->out_counts || !d->out_status)
+    return fail(DSV41_E_INVALID, "sampler shard: out_keys, out_counts and out_status are required");
+  Params p = make_params(sd, pl, nullptr);
+  p.voff = (int)d->vocab_offset;
+  p.vfull = (int)d->vocab_size;
+  p.emit_cap = d->max_candidates;
+  p.emit_keys = d->out_keys;
+  p.emit_count = d->out_counts;
+  p.out_status = d->out_status;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.esize == 2)
+    return pl.vec ? launch(topk_kernel<uint16_t, true, true>, TOPK_NT, pl.lds, sd->rows, p, s)
+                  : launch(topk_kernel<uint16_t, false, true>, TOPK_NT, pl.lds, sd->rows, p, s);
+  return pl.vec ? launch(topk_kernel<float, true, true>, TOPK_NT, pl.lds, sd->rows, p, s)
+                : launch(topk_kernel<float, false, true>, TOPK_NT, pl.lds, sd->rows, p, s);
+}
+
+extern "C" int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* d, void* stream) {
+  if (!d) return fail(DSV41_E_INVALID, "sampler merge descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_sampler_merge_desc))
+    return fail(DSV41_E_ABI, "dsv41_sampler_merge_desc size mismatch (rebuild the binding)");
+  if (d->rows <= 0 || d->n_shards <= 0 || d->max_candidates <= 0)
+    return fail(DSV41_E_INVALID, "sampler merge: rows, n_shards and max_candidates must be positive");
+  if (!(d->top_k >= 1 && d->top_k <= KCAP)) return fail(DSV41_E_INVALID, "sampler merge: top_k must be in [1, 2048]");
+  if (!(d->top_p > 0.0f && d->top_p <= 1.0f)) return fail(DSV41_E_INVALID, "top_p must be in (0, 1]");
+  if (!(d->min_p >= 0.0f && d->min_p <= 1.0f)) return fail(DSV41_E_INVALID, "min_p must be in [0, 1]");
+  if (!d->greedy && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
+  if (!d->keys || !d->counts || !d->status || !d->out_ids || !d->out_logprob || !d->out_status)
+    return fail(DSV41_E_INVALID, "sampler merge: keys, counts, status, out_ids, out_logprob and out_status are required");
+  const int64_t cap = (int64_t)d->n_shards * std::min<int64_t>(d->max_candidates, d->top_k);
+  const size_t lds = align16(sizeof(Misc)) + (256 + (size_t)cap + (size_t)d->top_k) * sizeof(uint64_t);
+  if (lds > LDS_LIMIT) return fail(DSV41_E_UNSUPPORTED, "sampler merge: n_shards * top_k exceeds the on-chip candidate buffer");
+  Params p{};
+  p.uniforms = d->uniforms;
+  p.out_ids = d->out_ids;
+  p.out_lp = d->out_logprob;
+  p.out_kept = d->out_kept;
+  p.out_status = d->out_status;
+  p.log_min_p = d->min_p > 0.0f ? std::log((double)d->min_p) : -INFINITY;
+  p.min_p = d->min_p;
+  p.top_p = d->top_p;
+  p.top_k = d->top_k;
+  p.greedy = d->greedy ? 1 : 0;
+  MergeIn in{d->keys, d->counts, d->status, d->n_shards, d->rows, d->max_candidates,
+             std::min(d->max_candidates, d->top_k)};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  DSV41_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(merge_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT));
+  hipLaunchKernelGGL(merge_kernel, dim3(d->rows), dim3(TOPK_NT), lds, s, p, in);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
 }

@@ -191,6 +191,44 @@ class LogprobCombineDesc(ctypes.Structure):
     ]
 
 
+class SamplerShardDesc(ctypes.Structure):
+    """dsv41_sampler_shard_desc: one vocabulary slice of a sharded sampling batch."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("max_candidates", ctypes.c_int32),
+        ("sampler", ctypes.POINTER(SamplerDesc)),
+        ("vocab_offset", ctypes.c_int64),
+        ("vocab_size", ctypes.c_int64),
+        ("out_keys", ctypes.c_void_p),
+        ("out_counts", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+    ]
+
+
+class SamplerMergeDesc(ctypes.Structure):
+    """dsv41_sampler_merge_desc: the exact finish of a sharded batch."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("rows", ctypes.c_int32),
+        ("n_shards", ctypes.c_int32),
+        ("max_candidates", ctypes.c_int32),
+        ("keys", ctypes.c_void_p),
+        ("counts", ctypes.c_void_p),
+        ("status", ctypes.c_void_p),
+        ("uniforms", ctypes.c_void_p),
+        ("top_k", ctypes.c_int32),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("greedy", ctypes.c_int32),
+        ("out_ids", ctypes.c_void_p),
+        ("out_logprob", ctypes.c_void_p),
+        ("out_kept", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+    ]
+
+
 EXPORTS = (
     "dsv41_abi_version",
     "dsv41_sampler_desc_size",
@@ -200,6 +238,8 @@ EXPORTS = (
     "dsv41_grpo_desc_size",
     "dsv41_logprob_shard_desc_size",
     "dsv41_logprob_combine_desc_size",
+    "dsv41_sampler_shard_desc_size",
+    "dsv41_sampler_merge_desc_size",
     "dsv41_last_error",
     "dsv41_sampler_workspace_bytes",
     "dsv41_sampler_run",
@@ -213,6 +253,8 @@ EXPORTS = (
     "dsv41_logprob_shard_workspace_bytes",
     "dsv41_logprob_shard_run",
     "dsv41_logprob_combine_run",
+    "dsv41_sampler_shard_run",
+    "dsv41_sampler_merge_run",
 )
 
 _lock = threading.Lock()
@@ -228,6 +270,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_grpo_desc_size.restype = ctypes.c_size_t
     lib.dsv41_logprob_shard_desc_size.restype = ctypes.c_size_t
     lib.dsv41_logprob_combine_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_sampler_shard_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_sampler_merge_desc_size.restype = ctypes.c_size_t
     lib.dsv41_last_error.restype = ctypes.c_char_p
     lib.dsv41_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.dsv41_sampler_workspace_bytes.argtypes = [ctypes.POINTER(SamplerDesc)]
@@ -257,6 +301,10 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
                                             ctypes.c_void_p]
     lib.dsv41_logprob_combine_run.restype = ctypes.c_int
     lib.dsv41_logprob_combine_run.argtypes = [ctypes.POINTER(LogprobCombineDesc), ctypes.c_void_p]
+    lib.dsv41_sampler_shard_run.restype = ctypes.c_int
+    lib.dsv41_sampler_shard_run.argtypes = [ctypes.POINTER(SamplerShardDesc), ctypes.c_void_p]
+    lib.dsv41_sampler_merge_run.restype = ctypes.c_int
+    lib.dsv41_sampler_merge_run.argtypes = [ctypes.POINTER(SamplerMergeDesc), ctypes.c_void_p]
     return lib
 
 
@@ -287,6 +335,10 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("dsv41_logprob_shard_desc layout differs between library and binding")
         if lib.dsv41_logprob_combine_desc_size() != ctypes.sizeof(LogprobCombineDesc):
             raise RuntimeError("dsv41_logprob_combine_desc layout differs between library and binding")
+        if lib.dsv41_sampler_shard_desc_size() != ctypes.sizeof(SamplerShardDesc):
+            raise RuntimeError("dsv41_sampler_shard_desc layout differs between library and binding")
+        if lib.dsv41_sampler_merge_desc_size() != ctypes.sizeof(SamplerMergeDesc):
+            raise RuntimeError("dsv41_sampler_merge_desc layout differs between library and binding")
         _lib = lib
         return lib
 

@@ -60,6 +60,56 @@ def _status_error(status: torch.Tensor) -> None:
         raise ValueError("uniforms must lie in [0, 1)")
 
 
+def _rows_in(logits, history, history_lens, temperature, top_k):
+    """Validated, GPU-resident logits [rows, V] and history of one batch."""
+    validate_temperature(temperature)
+    if not isinstance(logits, torch.Tensor) or logits.ndim != 2 or 0 in logits.shape:
+        raise ValueError("logits must have shape [rows, vocabulary_size]")
+    if not logits.is_cuda:
+        raise ValueError("logits must be on the GPU (libdsv41hip has no CPU path)")
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        logits = logits.float()
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    if isinstance(top_k, bool) or not isinstance(top_k, int) or top_k < 0:
+        raise ValueError("top_k must be a nonnegative integer")
+    rows = logits.shape[0]
+    if history is not None:
+        if history.ndim != 2 or history.shape[0] != rows:
+            raise ValueError("history must have shape [rows, history_length]")
+        history = history.to(device=logits.device, dtype=torch.int64)
+        if history.stride(1) != 1:
+            history = history.contiguous()
+        if history_lens is not None:
+            history_lens = history_lens.to(device=logits.device, dtype=torch.int32).contiguous()
+            if history_lens.shape != (rows,):
+                raise ValueError("history_lens must have one length per row")
+    return logits, history, history_lens
+
+
+def _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+               frequency_penalty, top_k, top_p, min_p) -> _lib.SamplerDesc:
+    desc = _lib.SamplerDesc()
+    desc.struct_size = _lib.ctypes.sizeof(_lib.SamplerDesc)
+    desc.rows, desc.vocab = logits.shape
+    desc.logits_dtype = _lib.DTYPE_F32 if logits.dtype == torch.float32 else _lib.DTYPE_BF16
+    desc.logits_row_stride = logits.stride(0)
+    desc.logits = logits.data_ptr()
+    if history is not None and history.shape[1] > 0:
+        desc.history = history.data_ptr()
+        desc.history_row_stride = history.stride(0)
+        desc.hist_len = history.shape[1]
+        desc.history_lens = _device_ptr(history_lens)
+    desc.temperature = temperature
+    desc.repetition_penalty = repetition_penalty
+    desc.presence_penalty = presence_penalty
+    desc.frequency_penalty = frequency_penalty
+    desc.top_k = top_k
+    desc.top_p = top_p
+    desc.min_p = min_p
+    return desc
+
+
 def sample(
     logits: torch.Tensor,
     *,
@@ -92,17 +142,7 @@ def sample(
     the reference's token (rollout.py:147-148) and leaves ``g`` where the reference leaves it.
     Only without top-k / top-p / min-p.
     """
-    validate_temperature(temperature)
-    if not isinstance(logits, torch.Tensor) or logits.ndim != 2 or 0 in logits.shape:
-        raise ValueError("logits must have shape [rows, vocabulary_size]")
-    if not logits.is_cuda:
-        raise ValueError("logits must be on the GPU (libdsv41hip has no CPU path)")
-    if logits.dtype not in (torch.float32, torch.bfloat16):
-        logits = logits.float()
-    if logits.stride(1) != 1:
-        logits = logits.contiguous()
-    if isinstance(top_k, bool) or not isinstance(top_k, int) or top_k < 0:
-        raise ValueError("top_k must be a nonnegative integer")
+    logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, top_k)
     rows, vocab = logits.shape
     device = logits.device
     if exponentials is not None and not greedy:
@@ -120,40 +160,13 @@ def sample(
         uniforms = uniforms.to(device=device, dtype=torch.float32).contiguous()
         if uniforms.shape != (rows,):
             raise ValueError("one uniform is required per row")
-    if history is not None:
-        if history.ndim != 2 or history.shape[0] != rows:
-            raise ValueError("history must have shape [rows, history_length]")
-        history = history.to(device=device, dtype=torch.int64)
-        if history.stride(1) != 1:
-            history = history.contiguous()
-        if history_lens is not None:
-            history_lens = history_lens.to(device=device, dtype=torch.int32).contiguous()
-            if history_lens.shape != (rows,):
-                raise ValueError("history_lens must have one length per row")
     ids = torch.empty(rows, dtype=torch.int64, device=device)
     lps = torch.empty(rows, dtype=torch.float32, device=device)
     kept = torch.empty(rows, dtype=torch.int32, device=device)
     status = torch.empty(rows, dtype=torch.int32, device=device)
-    desc = _lib.SamplerDesc()
-    desc.struct_size = _lib.ctypes.sizeof(_lib.SamplerDesc)
-    desc.rows = rows
-    desc.vocab = vocab
-    desc.logits_dtype = _lib.DTYPE_F32 if logits.dtype == torch.float32 else _lib.DTYPE_BF16
-    desc.logits_row_stride = logits.stride(0)
-    desc.logits = logits.data_ptr()
-    if history is not None and history.shape[1] > 0:
-        desc.history = history.data_ptr()
-        desc.history_row_stride = history.stride(0)
-        desc.hist_len = history.shape[1]
-        desc.history_lens = _device_ptr(history_lens)
+    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                      frequency_penalty, top_k, top_p, min_p)
     desc.uniforms = _device_ptr(uniforms)
-    desc.temperature = temperature
-    desc.repetition_penalty = repetition_penalty
-    desc.presence_penalty = presence_penalty
-    desc.frequency_penalty = frequency_penalty
-    desc.top_k = top_k
-    desc.top_p = top_p
-    desc.min_p = min_p
     desc.greedy = 1 if greedy else 0
     desc.out_ids = ids.data_ptr()
     desc.out_logprob = lps.data_ptr()
@@ -200,3 +213,116 @@ def sample_next(logits: torch.Tensor, temperature: float,
     else:
         raise ValueError("draw must be 'inverse_cdf' or 'exponential_race'")
     return int(result.ids.item()), float(result.logprobs.item())
+
+
+@dataclass
+class ShardCandidates:
+    """What one vocabulary slice contributes to a sharded batch, and what one all-gather
+    carries: the slice's candidate keys (int64 [rows, capacity], the bit patterns of the u64
+    keys of ``dsv41_sampler_shard_desc``), their counts (int32 [rows]) and the status bits
+    the slice saw (int32 [rows])."""
+
+    keys: torch.Tensor
+    counts: torch.Tensor
+    status: torch.Tensor
+
+
+def sample_shard(
+    logits: torch.Tensor,
+    *,
+    vocab_offset: int,
+    vocab_size: int,
+    top_k: int,
+    temperature: float = 1.0,
+    history: Optional[torch.Tensor] = None,
+    history_lens: Optional[torch.Tensor] = None,
+    repetition_penalty: float = 1.0,
+    presence_penalty: float = 0.0,
+    frequency_penalty: float = 0.0,
+    top_p: float = 1.0,
+    min_p: float = 0.0,
+) -> ShardCandidates:
+    """First half of sampling a vocabulary-sharded batch: this GPU's logits cover the ids
+    ``[vocab_offset, vocab_offset + logits.shape[1])`` of a ``vocab_size`` vocabulary (a
+    tensor-parallel head), the knobs are the batch's, and ``history`` holds global ids.
+    Returns the slice's exact local top-k under its local min-p bound; gather the results of
+    all slices and finish with :func:`merge_shards`.  Needs 1 <= top_k <= 2048 (the lists
+    then bound what the exchange carries)."""
+    logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, top_k)
+    rows, width = logits.shape
+    if top_k < 1:
+        raise ValueError("vocabulary-sharded sampling needs top_k >= 1")
+    if not (0 <= vocab_offset and vocab_offset + width <= vocab_size):
+        raise ValueError("the slice must lie within the vocabulary")
+    device = logits.device
+    keys = torch.empty(rows, top_k, dtype=torch.int64, device=device)
+    counts = torch.empty(rows, dtype=torch.int32, device=device)
+    status = torch.empty(rows, dtype=torch.int32, device=device)
+    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                      frequency_penalty, top_k, top_p, min_p)
+    shard = _lib.SamplerShardDesc()
+    shard.struct_size = _lib.ctypes.sizeof(_lib.SamplerShardDesc)
+    shard.max_candidates = top_k
+    shard.sampler = _lib.ctypes.pointer(desc)
+    shard.vocab_offset = vocab_offset
+    shard.vocab_size = vocab_size
+    shard.out_keys, shard.out_counts, shard.out_status = keys.data_ptr(), counts.data_ptr(), status.data_ptr()
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_shard_run(_lib.ctypes.byref(shard), stream)
+    _lib.check(rc)
+    return ShardCandidates(keys, counts, status)
+
+
+def merge_shards(
+    shards: list[ShardCandidates],
+    *,
+    top_k: int,
+    top_p: float = 1.0,
+    min_p: float = 0.0,
+    uniforms: Optional[torch.Tensor] = None,
+    generator: Optional[torch.Generator] = None,
+    greedy: bool = False,
+    check: bool = True,
+) -> SampleResult:
+    """Second half of sampling a vocabulary-sharded batch: the exact final selection (min-p,
+    top-k, top-p, draw) over the gathered candidate lists, with the knobs of the
+    :func:`sample_shard` calls.  Returns what :func:`sample` returns for the unsharded
+    logits; uniforms and checks behave as there."""
+    if not shards:
+        raise ValueError("merge_shards needs the lists of at least one slice")
+    keys = torch.stack([s.keys for s in shards]).contiguous()
+    counts = torch.stack([s.counts for s in shards]).contiguous()
+    status = torch.stack([s.status for s in shards]).contiguous()
+    n_shards, rows, cap = keys.shape
+    device = keys.device
+    if not greedy:
+        if uniforms is None:
+            if generator is not None and generator.device.type != "cpu":
+                raise ValueError("generation requires a CPU torch.Generator")
+            uniforms = torch.rand(rows, generator=generator, dtype=torch.float32)
+        uniforms = uniforms.to(device=device, dtype=torch.float32).contiguous()
+        if uniforms.shape != (rows,):
+            raise ValueError("one uniform is required per row")
+    ids = torch.empty(rows, dtype=torch.int64, device=device)
+    lps = torch.empty(rows, dtype=torch.float32, device=device)
+    kept = torch.empty(rows, dtype=torch.int32, device=device)
+    out_status = torch.empty(rows, dtype=torch.int32, device=device)
+    d = _lib.SamplerMergeDesc()
+    d.struct_size = _lib.ctypes.sizeof(_lib.SamplerMergeDesc)
+    d.rows, d.n_shards, d.max_candidates = rows, n_shards, cap
+    d.keys, d.counts, d.status = keys.data_ptr(), counts.data_ptr(), status.data_ptr()
+    d.uniforms = _device_ptr(uniforms if not greedy else None)
+    d.top_k, d.top_p, d.min_p, d.greedy = top_k, top_p, min_p, 1 if greedy else 0
+    d.out_ids, d.out_logprob, d.out_kept, d.out_status = (ids.data_ptr(), lps.data_ptr(), kept.data_ptr(),
+                                                          out_status.data_ptr())
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_merge_run(_lib.ctypes.byref(d), stream)
+    _lib.check(rc)
+    if check:
+        if bool((out_status != 0).any()):
+            _status_error(out_status)
+    return SampleResult(ids, lps, kept, out_status)
