@@ -373,10 +373,16 @@ __global__ __launch_bounds__(NT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
       // read zeros (offsets past the buffer); both stay unconditional so the multiplies
       // see one straight-line sequence.
       stage_setup();
+      // Raised priority for the k-step that carries the next loads: the SIMD's two waves
+      // leave the barrier together, and the one that falls behind in this k-step wins
+      // the issue arbitration until it drops back, so both reach the next barrier
+      // together instead of one idling there (measured: 24.5 -> 22.9 ms at D).
+      __builtin_amdgcn_s_setprio(1);
       mfma_set_x(acc, fa1, fb1, [&](int i) {
         frag_read(next, fch[0], fa0, fb0, i);
         if (i < A_LOADS + B_LOADS) issue_one(i);
       });
+      __builtin_amdgcn_s_setprio(0);
       advance();
     }
 
