@@ -1116,26 +1116,102 @@ __device__ __forceinline__ uint64_t uni(uint64_t v) {
          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
 }
 
+// The k-th largest of n unique u64 keys in LDS (1 <= k <= n): eight passes of an 8-bit
+// radix selection with u32 bin counts in cnt[256].
+template <int NT>
+__device__ __forceinline__ uint64_t kth_largest(const uint64_t* keys, int n, int k, uint32_t* cnt, Misc* m) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  uint64_t prefix = 0, mask = 0;
+  uint32_t target = (uint32_t)k;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += NT) cnt[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t key = keys[i];
+      if ((key & mask) == prefix) atomicAdd(&cnt[(key >> shift) & 255], 1u);
+    }
+    __syncthreads();
+    if (wid == 0) {
+      // bins in descending digit order: lane l holds digits 255-4l .. 252-4l
+      uint32_t c[4], sum = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        c[q] = cnt[255 - (lane * 4 + q)];
+        sum += c[q];
+      }
+      const uint32_t incl = (uint32_t)wave_incl_scan_i((int)sum, lane);
+      const uint32_t before = incl - sum;
+      if (before < target && target <= incl) {
+        uint32_t acc = before;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (acc < target && target <= acc + c[q]) {
+            m->bi[0] = 255 - (lane * 4 + q);
+            m->bi[1] = (int)(target - acc);
+          }
+          acc += c[q];
+        }
+      }
+    }
+    __syncthreads();
+    const int digit = uni(m->bi[0]);
+    target = (uint32_t)uni(m->bi[1]);
+    __syncthreads();
+    prefix |= (uint64_t)digit << shift;
+    mask |= (uint64_t)0xFF << shift;
+  }
+  return prefix;
+}
+
 // Keeps the candidate buffer at its top_k and within the min-p bound of mrun (a lower
-// bound of the row maximum); returns the new count and updates tau / tau_key.
+// bound of the row maximum); returns the new count and updates tau / tau_key.  The
+// top_k-th key comes from a radix selection (8 passes of 8 bits over the unique u64
+// keys), and the survivors are compacted in place, in buffer order: about 50x less LDS
+// traffic than sorting the buffer.  The buffer is left unsorted.
 template <int NT>
 __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, const Params& p, float mrun, float& tau,
-                            uint64_t& tau_key) {
-  const int tid = threadIdx.x;
-  bitonic_sort_desc<NT>(cand, n);
+                                            uint64_t& tau_key, uint64_t* hist) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const bool mp = p.min_p > 0.0f && mrun > NEG_INF;
   int el = n;
-  if (p.min_p > 0.0f && mrun > NEG_INF) {
+  if (mp) {
     int e = 0;
     for (int i = tid; i < n; i += NT) e += minp_ok(ckey_z(cand[i]), mrun, p) ? 1 : 0;
     el = block_sum_i<NT>(e, m);
   }
-  const int keep = uni(min(el, p.top_k));
-  if (keep == p.top_k && keep > 0) {
-    tau_key = uni(cand[keep - 1]);
-    tau = ckey_z(tau_key);
+  el = uni(el);
+  // With at least top_k keys inside the min-p bound the top_k largest keys survive (they
+  // pass it: the bound keeps a prefix of the key order); otherwise exactly those inside.
+  const bool by_key = el >= p.top_k && p.top_k > 0;
+  uint64_t thr = 0;
+  if (by_key) {
+    thr = uni(kth_largest<NT>(cand, n, p.top_k, reinterpret_cast<uint32_t*>(hist), m));
+    tau_key = thr;
+    tau = ckey_z(thr);
   }
-  __syncthreads();
-  return keep;
+  // In place, NT keys a round: a round reads its window [r0, r0 + NT), and its writes
+  // land below r0 + NT (at most r0 keys survive the earlier rounds), after every read of
+  // the window and before any read of the next one.
+  int total = 0;
+  for (int r0 = 0; r0 < n; r0 += NT) {
+    const int i = r0 + tid;
+    const uint64_t k = i < n ? cand[i] : 0;
+    const bool ok = i < n && (by_key ? k >= thr : (!mp || minp_ok(ckey_z(k), mrun, p)));
+    const unsigned long long bal = __ballot(ok);
+    if (lane == 0) m->ri[wid] = (int)__popcll(bal);
+    __syncthreads();
+    int before = 0, round = 0;
+    for (int w = 0; w < NT / 64; ++w) {
+      const int t = uni(m->ri[w]);
+      if (w < wid) before += t;
+      round += t;
+    }
+    if (ok) cand[total + before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] = k;
+    total += round;
+    __syncthreads();
+  }
+  return uni(total);
 }
 
 // Descending sort of 64*R u64 keys held by one wave, key at position r*64 + lane in
@@ -1390,7 +1466,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
     total = uni(total);
     before = uni(before);
     par ^= 1;
-    if (count + total > p.cap) count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key);
+    if (count + total > p.cap) count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key, hist);
     return count + total <= p.cap ? count + before : -1;
   };
   // One insertion round of up to M (<= G) elements per thread; always fits, because
