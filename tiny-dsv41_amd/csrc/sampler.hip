@@ -687,6 +687,17 @@ __device__ __forceinline__ float x_threshold(float tau, float bnd, const Params&
   return fmaxf(x_above(tau, p), x_above(next_down(bnd), p));
 }
 
+// RN(x / T): the three-operation scheme inside the range where it is exact (the guard of
+// make_z), IEEE division outside it.
+__device__ __forceinline__ float div_T(float x, const Params& p) {
+  const uint32_t a = __float_as_uint(x) & 0x7FFFFFFFu;
+  if (p.fast_div && a >= 0x0D800000u && a < 0x71800000u) {
+    const float q = x * p.rT;
+    return __builtin_fmaf(__builtin_fmaf(-q, p.T, x), p.rT, q);
+  }
+  return x / p.T;
+}
+
 // exact processed logit of a history token from its raw logit
 __device__ __forceinline__ float pen_z(float x, uint32_t c, const Params& p) {
   return penalize(x, c, p) / p.T;
@@ -1577,6 +1588,14 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
           // Every element above the running maximum passes, so the passers' largest z
           // keeps that maximum exact.
           float pz = NEG_INF;
+          // this lane's history bits of each tile, read together up front (the G
+          // elements of a lane share one bitmap word)
+          uint32_t hb[PF];
+#pragma unroll
+          for (int k = 0; k < PF; ++k) {
+            const int base = (t0 + k) * TILE + tid * G;
+            hb[k] = p.has_pen && base < p.V ? (h.bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u) : 0u;
+          }
 #pragma unroll
           for (int k = 0; k < PF; ++k) {
             const int base = (t0 + k) * TILE + tid * G;
@@ -1592,7 +1611,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
                   if (in && !isfinite(xv)) bad = 1;
                   ok = in && isfinite(xv);
                   if (ok) {
-                    if (p.has_pen && ((h.bitmap[idx >> 5] >> (idx & 31)) & 1u)) {
+                    if ((hb[k] >> j) & 1u) {
                       if (p.pen_lowers) {
                         const float z = pen_z(xv, p.freq != 0.0f ? count_of(h, slot_of(h, idx)) : 1u, p);
                         if (!isfinite(z)) bad = 1;
@@ -1603,7 +1622,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
                         ok = false;
                       }
                     } else {
-                      const float z = xv / p.T;
+                      const float z = div_T(xv, p);
                       pz = fmaxf(pz, z);
                       x[k][j] = z;
                     }
