@@ -37,7 +37,7 @@ BF16_PEAK_TFLOPS = 2500.0
 # profiles/logprob_backward_D.md.  Workloads without an entry report null.
 MEASURED_TRAFFIC = {
     "sampler_E": 2_630_896_096 + 2_473_704,  # topk_kernel + select_kernel
-    "logprob_D": 45_660_437_888 + 1_048_576,
+    "logprob_D": 46_112_195_686 + 1_048_576,
     "logprob_grad_D": 45_297_095_573 + 4_384_320_091,
 }
 
