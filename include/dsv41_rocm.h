@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define DSV41_ABI_VERSION 2
+#define DSV41_ABI_VERSION 3
 
 /* Element types of logits / activations. */
 #define DSV41_DTYPE_F32 0
@@ -57,6 +57,7 @@ extern "C" {
 #define DSV41_STATUS_BAD_HISTORY 2 /* a history id was >= vocab (id ignored)           */
 #define DSV41_STATUS_BAD_UNIFORM 4 /* uniform outside [0, 1) (row drawn with u = 0)    */
 #define DSV41_STATUS_RATIO_ZERO 8  /* Token-TIS raw weight exp(old - behaviour) == 0   */
+#define DSV41_STATUS_BAD_TARGET 16 /* a replay id was outside [0, vocab) (lp = NaN)    */
 
 /*
  * Row sampler.  For each row r of logits[rows, vocab]:
@@ -104,6 +105,11 @@ typedef struct dsv41_sampler_desc {
    * NULL: inverse CDF against uniforms. */
   const float* exponentials;       /* [rows, exponentials_row_stride] or NULL */
   int64_t exponentials_row_stride; /* in elements, >= vocab */
+  /* Replay (no truncation only): no draw; out_logprob[r] = the processed log-prob of token
+   * replay_ids[r], bit for bit the value a draw of that token reports on the same logits and
+   * knobs (behaviour log-probs replayed exactly, rl/qwen_policy.py:156-190); out_ids echoes
+   * the id.  uniforms may be NULL. */
+  const int64_t* replay_ids;       /* [rows] or NULL */
 } dsv41_sampler_desc;
 
 /*

@@ -84,6 +84,9 @@ def _sampler_desc(**kw):
     (dict(struct_size=8), _lib.E_ABI, "size mismatch"),
     (dict(exponentials=0x6000, exponentials_row_stride=100, top_k=5), _lib.E_UNSUPPORTED, "exponential race"),
     (dict(exponentials=0x6000, exponentials_row_stride=99), _lib.E_INVALID, "exponentials row stride"),
+    (dict(replay_ids=0x7000, top_k=5), _lib.E_UNSUPPORTED, "replay_ids"),
+    (dict(replay_ids=0x7000, min_p=0.1), _lib.E_UNSUPPORTED, "replay_ids"),
+    (dict(replay_ids=0x7000, exponentials=0x6000, exponentials_row_stride=100), _lib.E_UNSUPPORTED, "replay_ids"),
 ])
 def test_sampler_rejects_bad_descriptors_before_launch(kw, code, msg):
     lib = _lib.load()

@@ -1,0 +1,59 @@
+"""Replay of behaviour log-probs (a10): the reference requires the log-prob a policy reports
+when it replays an action to equal the one recorded when the action was sampled, bit for bit
+(tests/test_qwen_kv_cache.py:76-77 in the Tiny-DSV41 tree).  replay_log_probs on the same
+logits, temperature and penalties must return exactly the float that sample reported for the
+drawn token, whichever draw produced it; and it must agree with torch's
+log_softmax(logits / T)[token] within 1e-5 where no penalties apply.
+"""
+
+import pytest
+import torch
+
+from dsv41_rocm import replay_log_probs, sample, workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("name,rows,draw", [("B", 64, "cdf"), ("B", 64, "race"), ("B", 64, "greedy"),
+                                            ("E", 32, "cdf"), ("A", 8, "race")])
+def test_replay_equals_behaviour_bitwise(name, rows, draw):
+    inp = workloads.sampler_inputs(name, rows=rows, device=DEV)
+    x, h = inp["logits"], inp["history"]
+    pen = {k: v for k, v in inp["knobs"].items()
+           if k in ("temperature", "repetition_penalty", "presence_penalty", "frequency_penalty")}
+    print(f"case: config {name} rows {rows} draw {draw} knobs {pen}", flush=True)
+    g = torch.Generator().manual_seed(rows)
+    if draw == "race":
+        e = torch.empty(x.shape, dtype=torch.float32).exponential_(1, generator=g)
+        res = sample(x, history=h, exponentials=e, **pen)
+    elif draw == "greedy":
+        res = sample(x, history=h, greedy=True, **pen)
+    else:
+        res = sample(x, history=h, generator=g, **pen)
+    lp = replay_log_probs(x, res.ids, history=h, **pen)
+    assert torch.equal(lp, res.logprobs)
+
+
+def test_replay_matches_torch_log_softmax_and_any_token():
+    g = torch.Generator().manual_seed(4)
+    x = (3.0 * torch.randn(16, 50021, generator=g)).to(DEV)
+    tok = torch.randint(0, 50021, (16,), generator=g).to(DEV)
+    for T in (0.6, 1.0, 1.7):
+        lp = replay_log_probs(x, tok, temperature=T)
+        ref = torch.log_softmax(x.double() / T, dim=-1).gather(1, tok[:, None])[:, 0]
+        assert float((lp.double() - ref).abs().max()) <= 1e-5
+
+
+def test_replay_bad_ids_and_nonfinite_rows():
+    x = torch.randn(3, 1000, device=DEV)
+    with pytest.raises(ValueError, match="outside the model vocabulary"):
+        replay_log_probs(x, torch.tensor([0, 1000, 5]))
+    lp = replay_log_probs(x, torch.tensor([0, -1, 5]), check=False)
+    assert torch.isnan(lp[1]) and torch.isfinite(lp[0]) and torch.isfinite(lp[2])
+    x[2, 7] = float("nan")
+    with pytest.raises(ValueError, match="non-finite"):
+        replay_log_probs(x, torch.tensor([0, 1, 5]))
+    with pytest.raises(ValueError, match="one token ID"):
+        replay_log_probs(x, torch.tensor([0, 1]))

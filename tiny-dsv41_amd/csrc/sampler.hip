@@ -58,6 +58,13 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr int ST_NONFINITE = DSV41_STATUS_NONFINITE;
 constexpr int ST_BAD_HISTORY = DSV41_STATUS_BAD_HISTORY;
 constexpr int ST_BAD_UNIFORM = DSV41_STATUS_BAD_UNIFORM;
+constexpr int ST_BAD_TARGET = DSV41_STATUS_BAD_TARGET;
+constexpr int ST_RECHECK = 1 << 30;  // internal to topk_kernel: re-check every element of the row
+
+// full_kernel draws
+constexpr int DRAW_CDF = 0;     // inverse CDF against one uniform
+constexpr int DRAW_RACE = 1;    // exponential race against Exp(1) variates
+constexpr int DRAW_REPLAY = 2;  // no draw: the log-prob of a given token
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -76,6 +83,7 @@ struct Params {
   float* zbuf;
   const float* exps;  // exponential-race draw: [rows, estride] Exp(1) variates, or NULL
   int64_t estride;
+  const int64_t* replay;  // DRAW_REPLAY: the token of each row
   double log_min_p;
   float T, rT, rp, pres, freq, top_p, min_p, lmin_f;
   int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words, cap;
@@ -811,7 +819,7 @@ __device__ __forceinline__ Hist hist_tables(unsigned char* smem, const Layout& L
 // ====================================================================== FULL
 // No truncation: kept set = whole vocabulary.  Chunk c = [c*64G, (c+1)*64G) is one
 // wave's span of one tile; its (max, sum exp(z - max)) go to LDS.
-template <typename TIn, int G, bool VEC, bool RACE>
+template <typename TIn, int G, bool VEC, int DRAW>
 __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -891,7 +899,42 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   for (int s = tid; s < U; s += NT) atomicAdd(&cs[h.tok[s] / (64 * G)], exp2f((penz[s] - M) * LOG2E));
   __syncthreads();
 
-  if (RACE && !p.greedy) {
+  // Row total over the chunk table in one fixed order (lane l of wave 0 sums a contiguous
+  // run of chunks, then a wave scan): every draw reports its log-prob against this total,
+  // so that DRAW_REPLAY of the drawn token returns the same float bit for bit.
+  auto chunk_total = [&](double& incl, double& own) {
+    const int per = (NC + 63) / 64;
+    const int b = lane * per, e = min(b + per, NC);
+    double s = 0.0;
+    for (int c = b; c < e; ++c) s += (double)cs[c];
+    own = s;
+    incl = wave_incl_scan_d(s, lane);
+    return __shfl(incl, 63);
+  };
+
+  if constexpr (DRAW == DRAW_REPLAY) {
+    // the given token's processed log-prob (a separate instantiation, like the race)
+    if (wid == 0) {
+      double incl, own;
+      const double S = chunk_total(incl, own);
+      if (lane == 0) {
+        const int64_t tok = p.replay[row];
+        float lp = __builtin_nanf("");
+        if (tok >= 0 && tok < p.V) {
+          const int t = (int)tok;
+          const bool pen = p.has_pen && ((h.bitmap[t >> 5] >> (t & 31)) & 1u);
+          const float ztok = pen ? penz[slot_of(h, t)] : load_one<TIn>(rs, t) / p.T;
+          lp = (float)(((double)ztok - (double)M) - log(S));
+        } else {
+          m->status |= ST_BAD_TARGET;
+        }
+        write_result(p, row, m, tok, lp, p.V);
+      }
+    }
+    return;
+  }
+
+  if (DRAW == DRAW_RACE && !p.greedy) {
     // (a separate instantiation: the race's registers would cost the inverse-CDF draw occupancy)
     // Exponential race: the token is argmax_i p_i / E_i with p_i = exp(log_softmax(z)_i),
     // each step in fp32 as torch forms it (log_softmax = z - (max + log(sum)), exp,
@@ -955,14 +998,23 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
           b = m->rf[w];
           bi = m->ri[w];
         }
-      const int64_t tok = bi == 0x7FFFFFFF ? 0 : bi;
-      float ztok = M;
-      if (bi != 0x7FFFFFFF) {
-        const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
-        ztok = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
+      m->ri[0] = bi;
+    }
+    // the log-prob against the fixed-order total, as the other draws report it
+    if (wid == 0) {
+      double incl, own;
+      const double St = chunk_total(incl, own);
+      if (lane == 0) {
+        const int bi = m->ri[0];
+        const int64_t tok = bi == 0x7FFFFFFF ? 0 : bi;
+        float ztok = M;
+        if (bi != 0x7FFFFFFF) {
+          const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
+          ztok = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
+        }
+        const float lp = (float)(((double)ztok - (double)M) - log(St));
+        write_result(p, row, m, tok, lp, p.V);
       }
-      const float lp = (float)(((double)ztok - (double)M) - log(S));
-      write_result(p, row, m, tok, lp, p.V);
     }
     return;
   }
@@ -972,10 +1024,8 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   if (wid == 0) {
     const int per = (NC + 63) / 64;
     const int b = lane * per, e = min(b + per, NC);
-    double s = 0.0;
-    for (int c = b; c < e; ++c) s += (double)cs[c];
-    const double incl = wave_incl_scan_d(s, lane);
-    const double S = __shfl(incl, 63);
+    double s, incl;
+    const double S = chunk_total(incl, s);
     const double t = (double)u * S;
     double before = incl - s;
     int cstar = -1;
@@ -1700,9 +1750,9 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
   // re-check every element
   const float axw = wave_max_dpp(ax);
   const float pen_mag = p.has_pen ? axw * fmaxf(1.0f, p.rp) + fabsf(p.pres) + fabsf(p.freq) * (float)p.hstride : 0.0f;
-  if (!isfinite(axw / p.T) || !isfinite(pen_mag / p.T)) atomicOr(&m->status, 16);
+  if (!isfinite(axw / p.T) || !isfinite(pen_mag / p.T)) atomicOr(&m->status, ST_RECHECK);
   __syncthreads();
-  if (m->status & 16) {
+  if (m->status & ST_RECHECK) {
     for (int i = tid; i < p.V; i += NT) {
       const bool pen = p.has_pen && ((h.bitmap[i >> 5] >> (i & 31)) & 1u);
       const float xi = load_one<TIn>(rs, i);
@@ -1710,7 +1760,7 @@ __global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
       if (!isfinite(z)) bad = 1;
     }
     __syncthreads();
-    if (tid == 0) m->status &= ~16;
+    if (tid == 0) m->status &= ~ST_RECHECK;
   }
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
@@ -2020,7 +2070,8 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   if (d->top_k < 0) return fail(DSV41_E_INVALID, "top_k must be nonnegative");
   if (!(d->top_p > 0.0f && d->top_p <= 1.0f)) return fail(DSV41_E_INVALID, "top_p must be in (0, 1]");
   if (!(d->min_p >= 0.0f && d->min_p <= 1.0f)) return fail(DSV41_E_INVALID, "min_p must be in [0, 1]");
-  if (!shard && !d->greedy && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
+  if (!shard && !d->greedy && !d->uniforms && !d->replay_ids)
+    return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
   if (!shard && (!d->out_ids || !d->out_logprob || !d->out_status))
     return fail(DSV41_E_INVALID, "out_ids, out_logprob and out_status are required");
   const bool pen_on = d->repetition_penalty != 1.0f || d->presence_penalty != 0.0f || d->frequency_penalty != 0.0f;
@@ -2040,6 +2091,8 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
     return fail(DSV41_E_UNSUPPORTED, "exponential race draws need the full-vocabulary distribution (no top-k, top-p or min-p)");
   if (d->exponentials && d->exponentials_row_stride < d->vocab)
     return fail(DSV41_E_INVALID, "exponentials row stride must be >= vocab");
+  if (d->replay_ids && (truncating || d->exponentials || shard))
+    return fail(DSV41_E_UNSUPPORTED, "replay_ids take the full-vocabulary distribution (no top-k, top-p, min-p or exponentials)");
   // a vocabulary slice takes the TOPK kernel for any 1 <= top_k <= 2048: at or above the
   // slice width its buffer (top_k + 2048 keys) never compacts and it emits every survivor
   // of the local min-p bound
@@ -2085,6 +2138,7 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.zbuf = static_cast<float*>(workspace);
   p.exps = d->exponentials;
   p.estride = d->exponentials_row_stride;
+  p.replay = d->replay_ids;
   p.log_min_p = d->min_p > 0.0f ? std::log((double)d->min_p) : -INFINITY;
   {
     // log(min_p) as a float rounded toward -inf, for the conservative in-stream bound
@@ -2149,16 +2203,22 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
   const bool bf = pl.esize == 2;
   switch (pl.mode) {
     case MODE_FULL:
-      if (p.exps) {
-        if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, true>, FULL_NT, pl.lds, d->rows, p, s)
-                              : launch(full_kernel<uint16_t, 8, false, true>, FULL_NT, pl.lds, d->rows, p, s);
-        return pl.vec ? launch(full_kernel<float, 4, true, true>, FULL_NT, pl.lds, d->rows, p, s)
-                      : launch(full_kernel<float, 4, false, true>, FULL_NT, pl.lds, d->rows, p, s);
+      if (p.replay) {
+        if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
+                              : launch(full_kernel<uint16_t, 8, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 4, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
       }
-      if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, false>, FULL_NT, pl.lds, d->rows, p, s)
-                            : launch(full_kernel<uint16_t, 8, false, false>, FULL_NT, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(full_kernel<float, 4, true, false>, FULL_NT, pl.lds, d->rows, p, s)
-                    : launch(full_kernel<float, 4, false, false>, FULL_NT, pl.lds, d->rows, p, s);
+      if (p.exps) {
+        if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s)
+                              : launch(full_kernel<uint16_t, 8, false, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 4, false, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s);
+      }
+      if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
+                            : launch(full_kernel<uint16_t, 8, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
+      return pl.vec ? launch(full_kernel<float, 4, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
+                    : launch(full_kernel<float, 4, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
     case MODE_TOPK: {
       if (bf) rc = pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
                           : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);

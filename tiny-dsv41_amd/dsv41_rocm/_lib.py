@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).with_name("libdsv41hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -29,6 +29,7 @@ STATUS_NONFINITE = 1
 STATUS_BAD_HISTORY = 2
 STATUS_BAD_UNIFORM = 4
 STATUS_RATIO_ZERO = 8
+STATUS_BAD_TARGET = 16
 
 
 class SamplerDesc(ctypes.Structure):
@@ -60,6 +61,7 @@ class SamplerDesc(ctypes.Structure):
         ("out_status", ctypes.c_void_p),
         ("exponentials", ctypes.c_void_p),
         ("exponentials_row_stride", ctypes.c_int64),
+        ("replay_ids", ctypes.c_void_p),
     ]
 
 

@@ -58,6 +58,8 @@ def _status_error(status: torch.Tensor) -> None:
         raise ValueError("history token ID is outside the model vocabulary")
     if bits & _lib.STATUS_BAD_UNIFORM:
         raise ValueError("uniforms must lie in [0, 1)")
+    if bits & _lib.STATUS_BAD_TARGET:
+        raise ValueError("target token ID is outside the model vocabulary")
 
 
 def _rows_in(logits, history, history_lens, temperature, top_k):
@@ -326,3 +328,47 @@ def merge_shards(
         if bool((out_status != 0).any()):
             _status_error(out_status)
     return SampleResult(ids, lps, kept, out_status)
+
+
+def replay_log_probs(
+    logits: torch.Tensor,
+    token_ids: torch.Tensor,
+    *,
+    temperature: float = 1.0,
+    history: Optional[torch.Tensor] = None,
+    history_lens: Optional[torch.Tensor] = None,
+    repetition_penalty: float = 1.0,
+    presence_penalty: float = 0.0,
+    frequency_penalty: float = 0.0,
+    check: bool = True,
+) -> torch.Tensor:
+    """Processed log-prob of ``token_ids[r]`` under ``logits[r]`` for full-vocabulary sampling
+    (the reference's training-eligible mode), bit for bit what :func:`sample` reported when it
+    drew that token from the same logits with the same temperature and penalties, whichever
+    draw it used.  This is the replay the reference requires to equal the behaviour log-prob
+    exactly (``QwenPolicy.response_log_probs``, ``rl/qwen_policy.py:156-190``;
+    ``cached_response_log_probs``, ``backends/qwen_kv_cache.py:117-132``).  Returns fp32
+    ``[rows]``; with ``check`` raises the reference's ``ValueError`` for ids outside the
+    vocabulary and for non-finite rows."""
+    logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
+    rows = logits.shape[0]
+    device = logits.device
+    token_ids = torch.as_tensor(token_ids).to(device=device, dtype=torch.int64).reshape(-1).contiguous()
+    if token_ids.shape != (rows,):
+        raise ValueError("one token ID is required per row")
+    ids = torch.empty(rows, dtype=torch.int64, device=device)
+    lps = torch.empty(rows, dtype=torch.float32, device=device)
+    status = torch.empty(rows, dtype=torch.int32, device=device)
+    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                      frequency_penalty, 0, 1.0, 0.0)
+    desc.replay_ids = token_ids.data_ptr()
+    desc.out_ids, desc.out_logprob, desc.out_status = ids.data_ptr(), lps.data_ptr(), status.data_ptr()
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_run(_lib.ctypes.byref(desc), None, 0, stream)
+    _lib.check(rc)
+    if check:
+        if bool((status != 0).any()):
+            _status_error(status)
+    return lps
