@@ -102,6 +102,24 @@ def test_deferred_selection_mixed_rows(greedy):
     assert_exact(gpu, ora)
 
 
+@pytest.mark.parametrize("knobs", [dict(min_p=0.05), dict(min_p=0.1, top_p=0.97), dict(min_p=0.05, greedy=True)])
+def test_min_p_without_top_k_fast_path_and_fallback(knobs):
+    """min-p without top-k runs the top-k kernel with an internal bound of 1024; rows with more
+    min-p survivors (flat rows) are redone by the radix kernel.  300 rows, so the top-k rows also
+    take the deferred selection."""
+    g = torch.Generator().manual_seed(31)
+    rows, V = 300, 30011
+    logits = 4.0 * torch.randn(rows, V, generator=g)
+    logits[1::2] = 0.01 * torch.randn(rows // 2, V, generator=g)  # flat: every token survives min-p
+    logits[10, 3] = float("nan")
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, 128), generator=g)
+    greedy = knobs.get("greedy", False)
+    gpu, ora = run_both(logits, None if greedy else u, hist, repetition_penalty=1.2, temperature=0.8, **knobs)
+    assert_exact(gpu, ora)
+    assert (gpu[2][1::2][gpu[3][1::2] == 0] > 1024).all()  # the flat rows went through the fallback
+
+
 @pytest.mark.parametrize("knobs", [
     dict(temperature=0.9, top_p=0.9),                       # top-p without top-k (radix path)
     dict(temperature=1.3, min_p=0.02),                      # min-p only

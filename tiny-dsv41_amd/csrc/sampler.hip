@@ -49,6 +49,8 @@ constexpr int MAX_UNIQUE = 65535;              // history slots and counts are 1
 constexpr int DEFER_KEYS = 4 * 64;             // candidates a one-wave final selection holds
 constexpr int DEFER_MIN_ROWS = 256;            // batches above one row per CU defer it
 constexpr int SEL_WAVES = 4;                   // rows per select_kernel workgroup
+constexpr int INTERNAL_K = 1024;               // min-p without top-k: the bound topk_kernel keeps
+                                               // (its buffer then leaves room for two workgroups per CU)
 constexpr size_t LDS_LIMIT = 160 * 1024;
 
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -60,6 +62,7 @@ constexpr int ST_BAD_HISTORY = DSV41_STATUS_BAD_HISTORY;
 constexpr int ST_BAD_UNIFORM = DSV41_STATUS_BAD_UNIFORM;
 constexpr int ST_BAD_TARGET = DSV41_STATUS_BAD_TARGET;
 constexpr int ST_RECHECK = 1 << 30;  // internal to topk_kernel: re-check every element of the row
+constexpr int ST_FALLBACK = 1 << 29; // internal: an internal-k TOPK row needs generic_kernel
 
 // full_kernel draws
 constexpr int DRAW_CDF = 0;     // inverse CDF against one uniform
@@ -98,6 +101,10 @@ struct Params {
   int voff, vfull, emit_cap;
   uint64_t* emit_keys;  // [rows, emit_cap]
   int32_t* emit_count;  // [rows]
+  // min-p without top-k on topk_kernel: top_k holds an internal bound; a row that would
+  // cut its min-p survivors at it is flagged ST_FALLBACK and redone by generic_kernel,
+  // which then runs only on flagged rows (only_flagged)
+  int topk_internal, only_flagged;
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -1246,6 +1253,7 @@ __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, cons
   const bool by_key = el >= p.top_k && p.top_k > 0;
   uint64_t thr = 0;
   if (by_key) {
+    if (p.topk_internal && tid == 0) atomicOr(&m->status, ST_FALLBACK);
     thr = uni(kth_largest<NT>(cand, n, p.top_k, reinterpret_cast<uint32_t*>(hist), m));
     tau_key = thr;
     tau = ckey_z(thr);
@@ -1421,6 +1429,7 @@ __device__ __forceinline__ void block_final(const Params& p, int row, Misc* m, u
   int el = 0;
   for (int i = tid; i < n; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
   el = block_sum_i<NT>(el, m);
+  if (p.topk_internal && el > p.top_k && tid == 0) atomicOr(&m->status, ST_FALLBACK);
   const int K = min(p.top_k, el);
   uint64_t* q = cand + K;  // the keys past the top-k are not needed again
   for (int i = tid; i < K; i += NT) q[i] = mass_of(ckey_z(cand[i]), zmax);
@@ -1826,6 +1835,7 @@ __global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + L.hist256);
 
   const int row = blockIdx.x, tid = threadIdx.x;
+  if (p.only_flagged && !(p.out_status[row] & ST_FALLBACK)) return;
   HistIds<HR> hi;
   load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
@@ -2043,6 +2053,7 @@ struct Plan {
   bool vec;
   bool has_pen;
   bool defer;
+  bool internal_k;  // TOPK run for min-p without top-k, generic_kernel as the fallback
   int words, ucap, cap;
   size_t lds;
   size_t workspace;
@@ -2100,11 +2111,17 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   else if (!truncating) pl->mode = MODE_FULL;
   else if (d->top_k > 0 && d->top_k < V && d->top_k <= KCAP) pl->mode = MODE_TOPK;
   else pl->mode = MODE_GENERIC;
+  // min-p keeps the tokens near the row maximum: usually far fewer than INTERNAL_K, which
+  // TOPK handles exactly; rows that would need more go to generic_kernel
+  pl->internal_k = !shard && pl->mode == MODE_GENERIC && d->min_p > 0.0f && (d->top_k == 0 || d->top_k >= V) &&
+                   V > INTERNAL_K;
+  if (pl->internal_k) pl->mode = MODE_TOPK;
+  const int k_eff = pl->internal_k ? INTERNAL_K : d->top_k;
   pl->words = pl->has_pen ? (V + 31) / 32 : 0;
   pl->ucap = pl->has_pen ? (int)std::min<int64_t>(d->history_row_stride, V) : 0;
   if (pl->ucap > MAX_UNIQUE)
     return fail(DSV41_E_UNSUPPORTED, "history longer than 65535 ids per row is not supported");
-  pl->cap = pl->mode == MODE_TOPK ? d->top_k + TOPK_TILE : 0;
+  pl->cap = pl->mode == MODE_TOPK ? k_eff + TOPK_TILE : 0;
   Layout L;
   if (pl->mode == MODE_FULL)
     L = pl->esize == 4 ? make_layout<MODE_FULL, 4>(V, pl->words, pl->ucap, 0)
@@ -2117,9 +2134,15 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   if (pl->lds > LDS_LIMIT)
     return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
   pl->defer = !shard && pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
-  if (pl->mode == MODE_GENERIC) pl->workspace = (size_t)d->rows * (size_t)V * sizeof(float);
-  else if (pl->defer) pl->workspace = (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
-  else pl->workspace = 0;
+  pl->workspace = 0;
+  if (pl->defer) pl->workspace += (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
+  if (pl->mode == MODE_GENERIC || pl->internal_k) {
+    pl->workspace = align16(pl->workspace);  // the z rows follow the hand-over area
+    pl->workspace += (size_t)d->rows * (size_t)V * sizeof(float);
+    Layout Lg = make_layout<MODE_GENERIC, 4>(V, pl->words, pl->ucap, 0);
+    if (Lg.total > LDS_LIMIT)
+      return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
+  }
   return DSV41_OK;
 }
 
@@ -2136,6 +2159,9 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.out_kept = d->out_kept;
   p.out_status = d->out_status;
   p.zbuf = static_cast<float*>(workspace);
+  if (pl.defer && pl.internal_k)  // the z rows of the fallback follow the hand-over area
+    p.zbuf = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                      align16((size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t))));
   p.exps = d->exponentials;
   p.estride = d->exponentials_row_stride;
   p.replay = d->replay_ids;
@@ -2155,7 +2181,8 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.min_p = d->min_p;
   p.V = d->vocab;
   p.hlen = d->hist_len;
-  p.top_k = d->top_k;
+  p.top_k = pl.internal_k ? INTERNAL_K : d->top_k;
+  p.topk_internal = pl.internal_k ? 1 : 0;
   p.greedy = d->greedy ? 1 : 0;
   p.has_pen = pl.has_pen ? 1 : 0;
   p.pen_lowers = pl.has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&
@@ -2224,11 +2251,25 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
                           : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
       else rc = pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
                        : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
-      if (rc != DSV41_OK || !pl.defer) return rc;
-      hipLaunchKernelGGL(select_kernel, dim3((d->rows + SEL_WAVES - 1) / SEL_WAVES), dim3(SEL_WAVES * 64), 0, s,
-                         p, d->rows);
-      DSV41_HIP_CHECK(hipGetLastError());
-      return DSV41_OK;
+      if (rc != DSV41_OK) return rc;
+      if (pl.defer) {
+        hipLaunchKernelGGL(select_kernel, dim3((d->rows + SEL_WAVES - 1) / SEL_WAVES), dim3(SEL_WAVES * 64), 0, s,
+                           p, d->rows);
+        DSV41_HIP_CHECK(hipGetLastError());
+      }
+      if (!pl.internal_k) return DSV41_OK;
+      // rows flagged ST_FALLBACK (more min-p survivors than the internal bound) again,
+      // with generic_kernel; every other row returns at once
+      Params g = p;
+      g.top_k = d->top_k;
+      g.topk_internal = 0;
+      g.only_flagged = 1;
+      g.defer = 0;
+      const size_t lds = make_layout<MODE_GENERIC, 4>(d->vocab, pl.words, pl.ucap, 0).total;
+      if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, lds, d->rows, g, s)
+                            : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, lds, d->rows, g, s);
+      return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, lds, d->rows, g, s)
+                    : launch(generic_kernel<float, 4, false>, GEN_NT, lds, d->rows, g, s);
     }
     default:
       if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
