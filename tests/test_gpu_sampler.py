@@ -120,8 +120,48 @@ def test_min_p_without_top_k_fast_path_and_fallback(knobs):
     assert (gpu[2][1::2][gpu[3][1::2] == 0] > 1024).all()  # the flat rows went through the fallback
 
 
+@pytest.mark.parametrize("dtype,knobs", [
+    (torch.float32, dict(top_p=0.9)),
+    (torch.float32, dict(top_p=0.5, greedy=True)),
+    (torch.float32, dict(top_p=0.999, top_k=60000)),        # k >= V: top-p alone
+    (torch.bfloat16, dict(top_p=0.95)),
+])
+def test_top_p_alone_three_pass_kernel(dtype, knobs):
+    """Top-p without top-k or min-p: the row maximum, then exact masses into the total, bins of
+    (max - z) and a list of the tokens near the maximum; a third read where the list does not
+    reach the boundary bin.  Peaked rows finish from the list; flat and integer-valued (exact
+    ties) rows overflow it and take the third read; constant rows put every token in one bin,
+    above the 4096 the kernel holds, so the radix kernel redoes them.  A NaN row and a bad
+    uniform keep their statuses."""
+    g = torch.Generator().manual_seed(41)
+    rows, V = 48, 50021
+    logits = 3.0 * torch.randn(rows, V, generator=g)
+    logits[1::4] = 0.01 * torch.randn(rows // 4, V, generator=g)                 # flat
+    logits[2::4] = torch.randint(-4, 5, (rows // 4, V), generator=g).float()     # ties
+    logits[3::8] = 0.25                                                          # constant
+    logits[9, 77] = float("nan")
+    logits = logits.to(dtype)
+    u = torch.rand(rows, generator=g)
+    u[13] = -0.5
+    hist = torch.randint(0, V, (rows, 200), generator=g)
+    greedy = knobs.get("greedy", False)
+    gpu, ora = run_both(logits, None if greedy else u, hist, repetition_penalty=1.15, frequency_penalty=0.05,
+                        temperature=0.8, **knobs)
+    assert_exact(gpu, ora)
+    assert gpu[3][9] & 1 and (greedy or gpu[3][13] & 4)
+    if knobs["top_p"] < 0.99:
+        assert (gpu[2][3::8][gpu[3][3::8] == 0] > 4096).all()  # the constant rows went through the fallback
+
+
+def test_top_p_alone_config_e_vocabulary():
+    inp = workloads.sampler_inputs("E", rows=64)
+    gpu, ora = run_both(inp["logits"], inp["uniforms"], inp["history"], temperature=0.6,
+                        repetition_penalty=1.05, top_p=0.9)
+    assert_exact(gpu, ora)
+
+
 @pytest.mark.parametrize("knobs", [
-    dict(temperature=0.9, top_p=0.9),                       # top-p without top-k (radix path)
+    dict(temperature=0.9, top_p=0.9),                       # top-p without top-k (topp kernel)
     dict(temperature=1.3, min_p=0.02),                      # min-p only
     dict(temperature=0.8, top_k=6000, top_p=0.97),          # k above the one-pass capacity
     dict(temperature=0.7, top_k=3, min_p=0.2, top_p=0.5),

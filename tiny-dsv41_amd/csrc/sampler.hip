@@ -16,6 +16,10 @@
 //           has been seen, and the min-p bound of the running maximum) go to an LDS
 //           candidate buffer; after the pass the buffer is sorted and every decision
 //           (min-p, top-k, top-p, draw) is an exact scan over it.
+//   TOPP    (top-p alone): three streams of the row.  The first finds the maximum; the
+//           second sums every token's exact mass into the row total and into bins of
+//           the float bits of (max - z); the third collects the bin holding the top-p
+//           boundary and the kept mass of every 64*G-element chunk for the draw.
 //   GENERIC (anything else that truncates): z is written to a workspace row and the
 //           same decisions are made by exact radix selection over it.
 // History tokens are masked out of the stream and re-read per batch from the lines
@@ -35,6 +39,7 @@ namespace sampler {
 constexpr int MODE_FULL = 0;
 constexpr int MODE_TOPK = 1;
 constexpr int MODE_GENERIC = 2;
+constexpr int MODE_TOPP = 3;
 
 constexpr int FULL_NT = 1024;
 constexpr int TOPK_NT = 512;
@@ -51,6 +56,11 @@ constexpr int DEFER_MIN_ROWS = 256;            // batches above one row per CU d
 constexpr int SEL_WAVES = 4;                   // rows per select_kernel workgroup
 constexpr int INTERNAL_K = 1024;               // min-p without top-k: the bound topk_kernel keeps
                                                // (its buffer then leaves room for two workgroups per CU)
+constexpr int TOPP_NT = 1024;
+constexpr int TOPP_BINS = 4096;                // 32 octaves of (max - z) x 128 steps
+constexpr int TOPP_BIN_BASE = 100 << 7;        // octave 0 is [2^-27, 2^-26); smaller -> bin 0
+constexpr int TOPP_CAP = 4096;                 // list / boundary-bin tokens topp_kernel holds
+static_assert(TOPP_CAP <= TOPP_BINS, "the boundary bin's tokens from the list go to the bins' space");
 constexpr size_t LDS_LIMIT = 160 * 1024;
 
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -161,6 +171,7 @@ __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int ca
   l.mode0 = off;
   if (MODE == MODE_FULL) off += 8 * (size_t)n_chunks<G>(V);
   if (MODE == MODE_TOPK) off += 8 * (size_t)cap;
+  if (MODE == MODE_TOPP) off += 8 * ((size_t)TOPP_BINS + (size_t)n_chunks<G>(V) + (size_t)cap);
   l.total = align16(off);
   return l;
 }
@@ -1967,6 +1978,403 @@ __global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
   }
 }
 
+// ====================================================================== TOPP
+// Top-p without top-k or min-p.  The kept set is the shortest prefix of the (z desc,
+// index asc) order whose fixed-point mass reaches top_p_threshold(top_p, total), so the
+// total over the whole row is needed before any token can be placed.  The row is read
+// two or three times instead of being written to a workspace:
+//   1. z of every token (penalties exact), the row maximum and its first index;
+//   2. every token's exact mass (mass_of, zero below d = z - zmax = -30) into the row
+//      total and into a bin of the float bits of (zmax - z), and the tokens with d at
+//      or above a bound that rises as it fills into an LDS list.  fl(zmax - z) is
+//      monotone in z, so the bins split the descending order into consecutive runs.
+// The cumulative bin masses then name the bin b* holding the boundary.  Tokens of bins
+// before b* are kept (their masses go to the chunk table, one u64 per 64*G-element chunk
+// as in FULL, and to the exp sum); the tokens of b* are sorted and kept up to the first
+// prefix reaching the threshold.  Both sets come from the list when it covers every bin
+// up to b* (the bound stayed below b*'s range), else from a third read.  A b* above
+// TOPP_CAP tokens flags the row ST_FALLBACK for generic_kernel.
+// The draw scans the chunk table and re-reads one chunk.
+
+// The list's bound on d = z - zmax for a list of c tokens out of cap: it rises as the
+// list fills, so rows with many tokens near the maximum keep only the nearest.
+__device__ __forceinline__ float topp_list_bound(int c, int cap) {
+  const int e = c * 8 / cap;  // eighths of the list in use
+  return e < 1 ? (c * 16 < cap ? -16.0f : -12.0f) : e < 2 ? -8.0f : e < 3 ? -6.0f : e < 4 ? -4.0f
+       : e < 5 ? -3.0f : e < 6 ? -2.0f : -1.0f;
+}
+
+__device__ __forceinline__ int topp_bin(float z, float zmax) {
+  const int b = (int)(__float_as_uint(zmax - z) >> 16) - TOPP_BIN_BASE;
+  return min(max(b, 0), TOPP_BINS - 1);
+}
+
+template <typename TIn, int G, bool VEC>
+__global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
+  constexpr int NT = TOPP_NT, HR = 4, TILE = NT * G, CH = 64 * G;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const Layout L = make_layout<MODE_TOPP, G>(p.V, p.words, p.ucap, p.cap);
+  Misc* m = reinterpret_cast<Misc*>(smem + L.misc);
+  const Hist h = hist_tables(smem, L);
+  uint64_t* bins = reinterpret_cast<uint64_t*>(smem + L.mode0);
+  uint64_t* chunks = bins + TOPP_BINS;
+  const int nch = n_chunks<G>(p.V);
+  uint64_t* cand = chunks + nch;
+
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  HistIds<HR> hi;
+  load_history<NT, HR>(p, row, hi);
+  const TIn* src = row_ptr<TIn>(p, row);
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
+  const int V = p.V;
+
+  // ---- pass 1: maximum and its first index
+  int bad = 0, U = 0;
+  float bm = NEG_INF;
+  int bi = 0x7FFFFFFF;
+  stream_row<TIn, G, NT, VEC, false>(
+      p, rs, h,
+      [&]() {
+        if (tid == 0) {
+          m->status = 0;
+          m->count = 0;
+        }
+        for (int i = tid; i < TOPP_BINS; i += NT) bins[i] = 0;
+        for (int i = tid; i < nch; i += NT) chunks[i] = 0;
+        __syncthreads();
+        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        landed(hi);
+        return U;
+      },
+      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+          const int t = t0 + k;
+          if (t < nt) {
+            const int base = t * TILE + tid * G;
+            float x[G], z[G];
+            unpack(R[k], x);
+            make_z<G, true>(x, base, p, h.bitmap, z, bad);
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+              if (z[j] > bm) {
+                bm = z[j];
+                bi = base + j;
+              }
+          }
+        }
+        for (int i = tid; i < n; i += NT) {
+          const int s = s0 + i;
+          const int tok = (int)h.tok[s];
+          const float x = i == tid ? gx : load_one<TIn>(rs, tok);
+          const float z = pen_z(x, count_of(h, s), p);
+          if (!isfinite(z)) bad = 1;
+          if (z > bm || (z == bm && tok < bi)) {
+            bm = z;
+            bi = tok;
+          }
+        }
+      });
+  if (bad) atomicOr(&m->status, ST_NONFINITE);
+  const float zmax = block_max<NT>(bm, m);
+  int am = block_min_i<NT>(bm == zmax ? bi : 0x7FFFFFFF, m);
+  if (am < 0 || am >= V) am = 0;
+  const float u = row_uniform(p, row, m);
+  __syncthreads();
+  if (m->status & ST_NONFINITE) {
+    if (tid == 0) write_result(p, row, m, am, 0.0f, 0);
+    return;
+  }
+  const double dmax = (double)zmax;
+
+  // ---- pass 2: exact masses into the row total and the bins; tokens near the maximum
+  // into the list.  A thread lists a token when d >= its bound db, which only rises with
+  // the list's length, so the list holds every token with d >= (the largest final db).
+  uint64_t tot = 0;
+  float db = -16.0f;
+  int lost = 0;
+  auto offer = [&](float z, int idx) {
+    const int pos = atomicAdd(&m->count, 1);
+    if (pos < p.cap) cand[pos] = ckey(z, (uint32_t)idx);
+    else lost = 1;
+  };
+  auto pass_setup = [&]() { return U; };
+  stream_row<TIn, G, NT, VEC, false>(
+      p, rs, h, pass_setup,
+      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+          const int t = t0 + k;
+          if (t < nt) {
+            const int base = t * TILE + tid * G;
+            float x[G], z[G];
+            unpack(R[k], x);
+            make_z<G, true>(x, base, p, h.bitmap, z, bad);
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+              const double d = (double)z[j] - dmax;
+              if (d >= -30.0) {
+                const uint64_t ms = (uint64_t)(exp_det(d) * 8796093022208.0);
+                tot += ms;
+                if (ms) atomicAdd((unsigned long long*)&bins[topp_bin(z[j], zmax)], (unsigned long long)ms);
+                if (d >= (double)db) offer(z[j], base + j);
+              }
+            }
+            db = fmaxf(db, topp_list_bound(__atomic_load_n(&m->count, __ATOMIC_RELAXED), p.cap));
+          }
+        }
+        for (int i = tid; i < n; i += NT) {
+          const int s = s0 + i;
+          const int tok = (int)h.tok[s];
+          const float x = i == tid ? gx : load_one<TIn>(rs, tok);
+          const float z = pen_z(x, count_of(h, s), p);
+          const double d = (double)z - dmax;
+          if (d >= -30.0) {
+            const uint64_t ms = (uint64_t)(exp_det(d) * 8796093022208.0);
+            tot += ms;
+            if (ms) atomicAdd((unsigned long long*)&bins[topp_bin(z, zmax)], (unsigned long long)ms);
+            if (d >= (double)db) offer(z, tok);
+          }
+        }
+      });
+  tot = block_sum_u64<NT>(tot, m);  // its barriers also order the bin and list atomics
+  const uint64_t thr = top_p_threshold(p.top_p, tot);
+  const float dbf = block_max<NT>(db, m);
+  lost = block_sum_i<NT>(lost, m);
+  const int nl = min(m->count, p.cap);
+
+  // bin b* with (mass of bins < b*) < thr <= (mass of bins <= b*); the maximum's own
+  // mass (2^43, bin 0) makes it exist for every finite row
+  if (wid == 0) {
+    if (lane == 0) m->bi[0] = -1;
+    constexpr int PER = TOPP_BINS / 64;
+    uint64_t s = 0;
+    for (int q = 0; q < PER; ++q) s += bins[lane * PER + q];
+    const uint64_t incl = wave_incl_scan_u64(s, lane);
+    const uint64_t before = incl - s;
+    if (before < thr && thr <= incl) {
+      uint64_t acc = before;
+      for (int q = 0; q < PER; ++q) {
+        const uint64_t v = bins[lane * PER + q];
+        if (acc + v >= thr) {
+          m->bi[0] = lane * PER + q;
+          m->bu[0] = acc;
+          break;
+        }
+        acc += v;
+      }
+    }
+  }
+  __syncthreads();
+  const int bstar = m->bi[0];
+  const uint64_t cum_before = m->bu[0];
+  if (tid == 0) m->count = 0;
+  __syncthreads();
+
+  // The list covers bins <= b* when every token there has d >= dbf: such a token has
+  // fl(zmax - z) below the bin's upper edge ub, so d > -ub * (1 + 2^-23).
+  bool from_list = !lost && bstar >= 0 && bstar < TOPP_BINS - 1;
+  if (from_list) {
+    const float ub = __uint_as_float((uint32_t)(bstar + TOPP_BIN_BASE + 1) << 16);
+    from_list = (double)ub * (1.0 + 0x1p-22) <= -(double)dbf;
+  }
+  // the boundary bin's tokens, unsorted: from the list into the bins' space (free now),
+  // or from a third read into the list's space
+  uint64_t* blist = from_list ? bins : cand;
+  double es = 0.0;
+  int nk = 0;
+  if (from_list) {
+    for (int i = tid; i < nl; i += NT) {
+      const uint64_t key = cand[i];
+      const float z = ckey_z(key);
+      const int b = topp_bin(z, zmax);
+      if (b < bstar) {
+        const double e = exp_det((double)z - dmax);
+        atomicAdd((unsigned long long*)&chunks[ckey_idx(key) / CH], (unsigned long long)(e * 8796093022208.0));
+        es += e;
+        ++nk;
+      } else if (b == bstar) {
+        blist[atomicAdd(&m->count, 1)] = key;  // at most nl <= TOPP_CAP <= TOPP_BINS
+      }
+    }
+  } else {
+    // pass 3: kept masses per chunk, the boundary bin's tokens
+    stream_row<TIn, G, NT, VEC, false>(
+        p, rs, h, pass_setup,
+        [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+#pragma unroll
+          for (int k = 0; k < PF; ++k) {
+            const int t = t0 + k;
+            if (t < nt) {
+              const int base = t * TILE + tid * G;
+              float x[G], z[G];
+              unpack(R[k], x);
+              make_z<G, true>(x, base, p, h.bitmap, z, bad);
+              uint64_t cs = 0;
+#pragma unroll
+              for (int j = 0; j < G; ++j) {
+                const double d = (double)z[j] - dmax;
+                if (d >= -30.0) {
+                  const int b = topp_bin(z[j], zmax);
+                  if (b < bstar) {
+                    const double e = exp_det(d);
+                    cs += (uint64_t)(e * 8796093022208.0);
+                    es += e;
+                    ++nk;
+                  } else if (b == bstar) {
+                    const int pos = atomicAdd(&m->count, 1);
+                    if (pos < p.cap) cand[pos] = ckey(z[j], (uint32_t)(base + j));
+                  }
+                }
+              }
+              if (__builtin_amdgcn_ballot_w64(cs != 0)) {
+                cs = wave_sum_u64(cs);
+                if (lane == 0) atomicAdd((unsigned long long*)&chunks[t * (NT / 64) + wid], (unsigned long long)cs);
+              }
+            }
+          }
+          for (int i = tid; i < n; i += NT) {
+            const int s = s0 + i;
+            const int tok = (int)h.tok[s];
+            const float x = i == tid ? gx : load_one<TIn>(rs, tok);
+            const float z = pen_z(x, count_of(h, s), p);
+            const double d = (double)z - dmax;
+            if (d >= -30.0) {
+              const int b = topp_bin(z, zmax);
+              if (b < bstar) {
+                const double e = exp_det(d);
+                atomicAdd((unsigned long long*)&chunks[tok / CH], (unsigned long long)(e * 8796093022208.0));
+                es += e;
+                ++nk;
+              } else if (b == bstar) {
+                const int pos = atomicAdd(&m->count, 1);
+                if (pos < p.cap) cand[pos] = ckey(z, (uint32_t)tok);
+              }
+            }
+          }
+        });
+  }
+  __syncthreads();
+  const int nc = m->count;
+  if (nc > p.cap || bstar < 0) {
+    if (tid == 0) p.out_status[row] = m->status | ST_FALLBACK;
+    return;
+  }
+  // the boundary inside b*: the first prefix of its sorted tokens reaching thr
+  bitonic_sort_desc<NT>(blist, nc);
+  __syncthreads();
+  if (wid == 0) {
+    uint64_t carry = cum_before;
+    int js = nc - 1;
+    for (int c0 = 0; c0 < nc; c0 += 64) {
+      const int j = c0 + lane;
+      const uint64_t ms = j < nc ? mass_of(ckey_z(blist[j]), zmax) : 0;
+      const uint64_t incl = wave_incl_scan_u64(ms, lane) + carry;
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(j < nc && incl >= thr);
+      if (hit) {
+        js = c0 + __builtin_ctzll(hit);
+        break;
+      }
+      carry = __shfl(incl, 63);
+    }
+    if (lane == 0) m->bi[1] = js;
+  }
+  __syncthreads();
+  const int jstar = m->bi[1];
+
+  // kept tokens of b*: blist[0..jstar]; every kept token has key >= blist[jstar]
+  for (int j = tid; j <= jstar; j += NT) {
+    const uint64_t key = blist[j];
+    const double e = exp_det((double)ckey_z(key) - dmax);
+    atomicAdd((unsigned long long*)&chunks[ckey_idx(key) / CH], (unsigned long long)(e * 8796093022208.0));
+    es += e;
+    ++nk;
+  }
+  const uint64_t Bkey = jstar >= 0 && jstar < nc ? blist[jstar] : ~0ull;
+  nk = block_sum_i<NT>(nk, m);
+  const double esum = block_sum_d<NT>(es, m);  // its barriers also order the chunk atomics
+
+  int64_t tok = am;
+  float ztok = zmax;
+  if (!p.greedy) {
+    uint64_t sk = 0;
+    for (int i = tid; i < nch; i += NT) sk += chunks[i];
+    sk = block_sum_u64<NT>(sk, m);
+    const uint64_t t = draw_target(u, sk);
+    block_incl_scan_u64<NT>(chunks, nch, m);
+    // first chunk whose inclusive mass exceeds t
+    for (int c = tid; c < nch; c += NT) {
+      const uint64_t before = c ? chunks[c - 1] : 0;
+      if (before <= t && t < chunks[c]) {
+        m->bi[2] = c;
+        m->bu[1] = before;
+      }
+    }
+    __syncthreads();
+    const int c = m->bi[2];
+    const uint64_t before = m->bu[1];
+    if (wid == 0) {
+      // re-read chunk c; kept = bin < b*, or bin b* at or above the boundary key
+      const int base = c * CH + lane * G;
+      uint64_t ms[G];
+      float zz[G];
+      uint64_t ls = 0;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const int idx = base + j;
+        float z = NEG_INF;
+        if (idx < V) {
+          const float x = load_one<TIn>(rs, idx);
+          if (p.has_pen && ((h.bitmap[idx >> 5] >> (idx & 31)) & 1u)) {
+            const int sl = slot_of(h, idx);
+            z = pen_z(x, count_of(h, sl), p);
+          } else {
+            z = div_T(x, p);
+          }
+        }
+        zz[j] = z;
+        ms[j] = 0;
+        const double d = (double)z - dmax;
+        if (d >= -30.0 && ckey(z, (uint32_t)idx) >= Bkey) ms[j] = (uint64_t)(exp_det(d) * 8796093022208.0);
+        ls += ms[j];
+      }
+      const uint64_t incl = wave_incl_scan_u64(ls, lane) + before;
+      uint64_t acc = incl - ls;
+      int pick = -1;
+      float zp = 0.0f;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        if (pick < 0 && ms[j] != 0 && t < acc + ms[j]) {
+          pick = base + j;
+          zp = zz[j];
+        }
+        acc += ms[j];
+      }
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(pick >= 0);
+      if (hit) {
+        const int src_lane = __builtin_ctzll(hit);
+        const int pk = __shfl(pick, src_lane);
+        const float zpk = __shfl(zp, src_lane);
+        if (lane == 0) {
+          m->bi[3] = pk;
+          m->bf[0] = zpk;
+        }
+      } else if (lane == 0) {
+        m->bi[3] = -1;
+      }
+    }
+    __syncthreads();
+    if (m->bi[3] >= 0) {
+      tok = m->bi[3];
+      ztok = m->bf[0];
+    }
+  }
+  if (tid == 0) {
+    const float lp = (float)(((double)ztok - dmax) - log(esum));
+    write_result(p, row, m, tok, lp, nk);
+  }
+}
+
 // One wave per deferred TOPK row: the final selection over the row's candidates,
 // exactly as topk_kernel runs it in place.  The row's status so far is in out_status.
 __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int rows) {
@@ -2054,6 +2462,7 @@ struct Plan {
   bool has_pen;
   bool defer;
   bool internal_k;  // TOPK run for min-p without top-k, generic_kernel as the fallback
+                    // (TOPP rows fall back to generic_kernel the same way)
   int words, ucap, cap;
   size_t lds;
   size_t workspace;
@@ -2121,13 +2530,20 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   pl->ucap = pl->has_pen ? (int)std::min<int64_t>(d->history_row_stride, V) : 0;
   if (pl->ucap > MAX_UNIQUE)
     return fail(DSV41_E_UNSUPPORTED, "history longer than 65535 ids per row is not supported");
-  pl->cap = pl->mode == MODE_TOPK ? k_eff + TOPK_TILE : 0;
+  // top-p alone: three streams of the row (topp_kernel) where its tables fit on chip
+  if (!shard && pl->mode == MODE_GENERIC && d->top_p < 1.0f && !(d->min_p > 0.0f) &&
+      (d->top_k == 0 || d->top_k >= V) &&
+      make_layout<MODE_TOPP, 4>(V, pl->words, pl->ucap, TOPP_CAP).total <= LDS_LIMIT)
+    pl->mode = MODE_TOPP;
+  pl->cap = pl->mode == MODE_TOPK ? k_eff + TOPK_TILE : pl->mode == MODE_TOPP ? TOPP_CAP : 0;
   Layout L;
   if (pl->mode == MODE_FULL)
     L = pl->esize == 4 ? make_layout<MODE_FULL, 4>(V, pl->words, pl->ucap, 0)
                        : make_layout<MODE_FULL, 8>(V, pl->words, pl->ucap, 0);
   else if (pl->mode == MODE_TOPK)
     L = make_layout<MODE_TOPK, TOPK_G>(V, pl->words, pl->ucap, pl->cap);
+  else if (pl->mode == MODE_TOPP)
+    L = make_layout<MODE_TOPP, 4>(V, pl->words, pl->ucap, pl->cap);
   else
     L = make_layout<MODE_GENERIC, 4>(V, pl->words, pl->ucap, 0);
   pl->lds = L.total;
@@ -2136,7 +2552,7 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   pl->defer = !shard && pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
   pl->workspace = 0;
   if (pl->defer) pl->workspace += (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
-  if (pl->mode == MODE_GENERIC || pl->internal_k) {
+  if (pl->mode == MODE_GENERIC || pl->mode == MODE_TOPP || pl->internal_k) {
     pl->workspace = align16(pl->workspace);  // the z rows follow the hand-over area
     pl->workspace += (size_t)d->rows * (size_t)V * sizeof(float);
     Layout Lg = make_layout<MODE_GENERIC, 4>(V, pl->words, pl->ucap, 0);
@@ -2218,6 +2634,23 @@ extern "C" size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* d) {
   return pl.workspace;
 }
 
+// Rows flagged ST_FALLBACK by topk_kernel (more min-p survivors than the internal bound)
+// or topp_kernel (a boundary bin above TOPP_CAP) again, with generic_kernel; every other
+// row returns at once.
+static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, hipStream_t s) {
+  Params g = p;
+  g.top_k = d->top_k;
+  g.topk_internal = 0;
+  g.only_flagged = 1;
+  g.defer = 0;
+  g.cap = 0;
+  const size_t lds = make_layout<MODE_GENERIC, 4>(d->vocab, pl.words, pl.ucap, 0).total;
+  if (pl.esize == 2) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, lds, d->rows, g, s)
+                                   : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, lds, d->rows, g, s);
+  return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, lds, d->rows, g, s)
+                : launch(generic_kernel<float, 4, false>, GEN_NT, lds, d->rows, g, s);
+}
+
 extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   Plan pl;
@@ -2258,19 +2691,15 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
         DSV41_HIP_CHECK(hipGetLastError());
       }
       if (!pl.internal_k) return DSV41_OK;
-      // rows flagged ST_FALLBACK (more min-p survivors than the internal bound) again,
-      // with generic_kernel; every other row returns at once
-      Params g = p;
-      g.top_k = d->top_k;
-      g.topk_internal = 0;
-      g.only_flagged = 1;
-      g.defer = 0;
-      const size_t lds = make_layout<MODE_GENERIC, 4>(d->vocab, pl.words, pl.ucap, 0).total;
-      if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, lds, d->rows, g, s)
-                            : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, lds, d->rows, g, s);
-      return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, lds, d->rows, g, s)
-                    : launch(generic_kernel<float, 4, false>, GEN_NT, lds, d->rows, g, s);
+      return run_flagged(d, pl, p, s);
     }
+    case MODE_TOPP:
+      if (bf) rc = pl.vec ? launch(topp_kernel<uint16_t, 4, true>, TOPP_NT, pl.lds, d->rows, p, s)
+                          : launch(topp_kernel<uint16_t, 4, false>, TOPP_NT, pl.lds, d->rows, p, s);
+      else rc = pl.vec ? launch(topp_kernel<float, 4, true>, TOPP_NT, pl.lds, d->rows, p, s)
+                       : launch(topp_kernel<float, 4, false>, TOPP_NT, pl.lds, d->rows, p, s);
+      if (rc != DSV41_OK) return rc;
+      return run_flagged(d, pl, p, s);
     default:
       if (bf) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
                             : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, pl.lds, d->rows, p, s);
