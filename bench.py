@@ -49,12 +49,14 @@ def sampler_bytes_per_row(vocab, esize, hist_len):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # A sampler step is about 0.5 ms: 100 timed steps after 20 warm-up steps measure the
+    # steady state (20 steps after 5 read several percent slow on a fresh box).
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="E", choices=["A", "B", "E", "none"],
                     help="sampler config; 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
-    ap.add_argument("--logprob-steps", type=int, default=5)
+    ap.add_argument("--logprob-steps", type=int, default=8)
     ap.add_argument("--no-backward", action="store_true", help="skip the log-prob backward timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -215,7 +217,7 @@ def main():
         line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
         print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
-        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 1, not args.no_cpu_baseline, torch,
+        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 2, not args.no_cpu_baseline, torch,
                                         backward=not args.no_backward)
     print(json.dumps(line), flush=True)
 
