@@ -1294,11 +1294,41 @@ __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, cons
   return uni(total);
 }
 
+// Lane exchange of a u64 with lane ^ j, all 64 lanes active.  j = 1, 2 and 8 are one
+// DPP move per half (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:8); j = 4 takes
+// row_ror:4 or row_ror:12, whichever brings lane ^ 4 (ror4 says so per lane); larger j
+// cross 16-lane rows and go through the LDS crossbar.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v, int j, bool ror4) {
+  switch (j) {
+    case 1:
+      return dpp_u64<0xB1>(v);
+    case 2:
+      return dpp_u64<0x4E>(v);
+    case 4: {
+      const uint64_t a = dpp_u64<0x124>(v), b = dpp_u64<0x12C>(v);
+      return ror4 ? a : b;
+    }
+    case 8:
+      return dpp_u64<0x128>(v);
+    default:
+      return __shfl_xor(v, j);
+  }
+}
+
 // Descending sort of 64*R u64 keys held by one wave, key at position r*64 + lane in
 // k[r], by the bitonic network (stride >= 64: within the lane; below: lane exchange).
 template <int R>
 __device__ __forceinline__ void wave_sort_desc(uint64_t (&k)[R], int lane) {
   constexpr int N = 64 * R;
+  const bool ror4 = dpp_u32<0x124>((uint32_t)lane) == (uint32_t)(lane ^ 4);
 #pragma unroll
   for (int s = 2; s <= N; s <<= 1) {
 #pragma unroll
@@ -1318,7 +1348,7 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&k)[R], int lane) {
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const uint64_t o = __shfl_xor(k[r], j);
+          const uint64_t o = lane_xor_u64(k[r], j, ror4);
           const bool desc = ((r * 64 + lane) & s) == 0;
           const bool lower = (lane & j) == 0;
           const bool take_max = lower == desc;
@@ -2377,8 +2407,15 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
 
 // One wave per deferred TOPK row: the final selection over the row's candidates,
 // exactly as topk_kernel runs it in place.  The row's status so far is in out_status.
+//
+// Every decision of the selection (top-k, top-p, the draw, the log-prob) is taken over
+// the candidates that pass min-p against the largest candidate, and those are a prefix
+// of the sorted order.  So the wave first keeps only those, in LDS, and sorts 64*R of
+// them with R chosen by their count: a row with 150 candidates of which 50 pass min-p
+// takes the one-key-per-lane sort.
 __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int rows) {
   __shared__ Misc ms[SEL_WAVES];
+  __shared__ uint64_t kept_keys[SEL_WAVES][DEFER_KEYS];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int row = blockIdx.x * SEL_WAVES + wid;
   if (row >= rows) return;
@@ -2391,9 +2428,36 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int ro
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const float u = row_uniform(p, row, m);
   const uint64_t* keys = p.defer_keys + (int64_t)row * DEFER_KEYS;
-  if (n <= 64) wave_final<1>(p, row, m, keys, n, u);
-  else if (n <= 128) wave_final<2>(p, row, m, keys, n, u);
-  else wave_final<4>(p, row, m, keys, n, u);
+  constexpr int RK = DEFER_KEYS / 64;
+  uint64_t k[RK];
+  uint64_t kmax = 0;
+#pragma unroll
+  for (int r = 0; r < RK; ++r) {
+    k[r] = r * 64 + lane < n ? keys[r * 64 + lane] : 0;  // 0 is below every key
+    kmax = k[r] > kmax ? k[r] : kmax;
+  }
+  // the largest key: its z is the row maximum the selection measures min-p against
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t t = __shfl_xor(kmax, o);
+    kmax = t > kmax ? t : kmax;
+  }
+  const float zmax = ckey_z(kmax);
+  uint64_t* buf = kept_keys[wid];
+  int el = 0;
+#pragma unroll
+  for (int r = 0; r < RK; ++r) {
+    const bool ok = r * 64 + lane < n && minp_ok(ckey_z(k[r]), zmax, p);
+    const unsigned long long b = __ballot(ok);
+    if (ok) buf[el + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u))] = k[r];
+    el += (int)__popcll(b);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (el <= 64) wave_final<1>(p, row, m, buf, el, u);
+  else if (el <= 128) wave_final<2>(p, row, m, buf, el, u);
+  else wave_final<4>(p, row, m, buf, el, u);
 }
 
 // One workgroup per row of a vocabulary-sharded batch: the final selection over the
