@@ -102,6 +102,35 @@ def test_deferred_selection_mixed_rows(greedy):
     assert_exact(gpu, ora)
 
 
+def test_deferred_selection_keeps_min_p_survivors_only():
+    """The deferred selection sorts only the candidates that pass min-p against the largest
+    one.  Rows of three kinds, 300 rows so the selection is deferred: about 200 early
+    candidates of which only the late maximum survives (one-key sort), 180 survivors
+    (four-key sort), and 100 survivors among 250 candidates (two-key sort)."""
+    g = torch.Generator().manual_seed(41)
+    rows, V = 300, 20011
+    logits = -20.0 + 0.01 * torch.randn(rows, V, generator=g)
+    for r in range(rows):
+        kind = r % 3
+        if kind == 0:  # early candidates, then a maximum that leaves them below min-p
+            logits[r, :200] = 0.1 * torch.randn(200, generator=g)
+            logits[r, V - 1 - r] = 10.0
+        elif kind == 1:  # 180 survivors spread over the row
+            idx = torch.randperm(V, generator=g)[:180]
+            logits[r, idx] = 5.0 + 0.1 * torch.randn(180, generator=g)
+        else:  # 150 early candidates below min-p, 100 survivors later
+            logits[r, :150] = 0.1 * torch.randn(150, generator=g)
+            logits[r, V // 2 : V // 2 + 100] = 6.0 + 0.1 * torch.randn(100, generator=g)
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, 64), generator=g)
+    knobs = dict(top_k=256, top_p=0.97, min_p=0.05, repetition_penalty=1.1)
+    gpu, ora = run_both(logits, u, hist, **knobs)
+    assert_exact(gpu, ora)
+    kept = gpu[2]
+    assert (kept[0::3] == 1).all()
+    assert (kept[1::3] > 128).all() and (kept[2::3] > 64).all()
+
+
 @pytest.mark.parametrize("knobs", [dict(min_p=0.05), dict(min_p=0.1, top_p=0.97), dict(min_p=0.05, greedy=True)])
 def test_min_p_without_top_k_fast_path_and_fallback(knobs):
     """min-p without top-k runs the top-k kernel with an internal bound of 1024; rows with more
