@@ -19,7 +19,11 @@
  *                         dsv41_train/rl/native_lora.py:80-82 (_score_targets),
  *                         plus the Token-TIS weight of dsv41_train/rl/algorithm.py:293-299.
  *   dsv41_sampler_shard_run + dsv41_sampler_merge_run <- the same lines for logits whose
- *                         vocabulary is split over tensor-parallel GPUs.
+ *                         vocabulary is split over tensor-parallel GPUs (top-k draws).
+ *   dsv41_sampler_full_state_run + dsv41_sampler_full_draw_run + dsv41_sampler_full_finish_run
+ *                      <- the same lines, the full-vocabulary draw of rollout.py:144-148
+ *                         (training's default, rollout_manager/training.py:74-81), over
+ *                         split vocabularies.
  *   dsv41_grpo_run     <- dsv41_train/rl/algorithm.py:169-246 (grpo_loss).
  *   dsv41_token_tis_run <- dsv41_train/rl/algorithm.py:249-346 (decoupled_token_tis_loss)
  *                         with the metric pooling of dsv41_train/rl/distributed_grpo.py:197-222.
@@ -38,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DSV41_ABI_VERSION 3
+#define DSV41_ABI_VERSION 4
 
 /* Element types of logits / activations. */
 #define DSV41_DTYPE_F32 0
@@ -136,6 +140,71 @@ typedef struct dsv41_sampler_shard_desc {
   int32_t* out_counts;               /* [rows] */
   int32_t* out_status;               /* [rows] DSV41_STATUS_* bits seen by this slice */
 } dsv41_sampler_shard_desc;
+
+/*
+ * Full-vocabulary draws (no top-k, top-p or min-p) over vocabulary slices, in three steps
+ * with one all-gather after each of the first two:
+ *   1. dsv41_sampler_full_state_run: each slice streams its columns once (penalties from the
+ *      global history ids, then / T) and writes one dsv41_full_state per row;
+ *   2. with the states of all slices gathered ([n_shards, rows], slices in vocabulary
+ *      order), dsv41_sampler_full_draw_run forms the row's maximum M and total
+ *      S = sum_s mass_s * exp(max_z_s - M) in slice order (fp64).  Inverse CDF: the slice
+ *      whose share of S holds u * S re-reads its columns and picks the token; the other
+ *      slices report none.  Exponential race: every slice reports its best p / E over its
+ *      columns with p = exp(z - (M + log S)) in fp32, first id on ties;
+ *   3. with the picks gathered, dsv41_sampler_full_finish_run writes ids, log-probs
+ *      lp = (z_tok - M) - log S, kept = vocab_size and status bits, as dsv41_sampler_run
+ *      does (greedy needs only the states: the first slice holding M gives its argmax).
+ * The states (32 bytes) and picks (16 bytes) per row and slice are the wire format.
+ */
+typedef struct dsv41_full_state {
+  float max_z;      /* the slice's largest processed logit; -inf when it has none */
+  int32_t status;   /* DSV41_STATUS_* bits seen by this slice */
+  double mass;      /* sum over the slice of exp(z - max_z), in the slice's fixed chunk order */
+  int64_t argmax;   /* global id of the slice's first largest logit */
+  int64_t reserved;
+} dsv41_full_state;
+
+typedef struct dsv41_full_pick {
+  int64_t id;       /* global id chosen by this slice, or -1 */
+  float z;          /* its processed logit */
+  float ratio;      /* exponential race: its p / E */
+} dsv41_full_pick;
+
+typedef struct dsv41_sampler_full_shard_desc {
+  uint32_t struct_size;              /* = sizeof(dsv41_sampler_full_shard_desc) */
+  int32_t n_shards;                  /* draw step: slices in `states` */
+  const dsv41_sampler_desc* sampler; /* the slice [rows, vocab] holding ids [vocab_offset,
+                                        vocab_offset + vocab); knobs without truncation;
+                                        draw step: uniforms, or exponentials over the slice's
+                                        columns (race); out_* unused */
+  int64_t vocab_offset;              /* global id of the slice's first column */
+  int64_t vocab_size;                /* the whole vocabulary; larger history ids flag the row */
+  int32_t shard_index;               /* draw step: this slice's position in `states` */
+  int32_t reserved;
+  const dsv41_full_state* states;    /* draw step: [n_shards, rows], gathered */
+  dsv41_full_state* out_states;      /* state step: [rows] */
+  dsv41_full_pick* out_picks;        /* draw step: [rows] */
+} dsv41_sampler_full_shard_desc;
+
+#define DSV41_FULL_DRAW_CDF 0     /* inverse CDF against uniforms */
+#define DSV41_FULL_DRAW_RACE 1    /* exponential race */
+#define DSV41_FULL_DRAW_GREEDY 2  /* first largest logit (no draw step) */
+
+typedef struct dsv41_sampler_full_finish_desc {
+  uint32_t struct_size;            /* = sizeof(dsv41_sampler_full_finish_desc) */
+  int32_t rows;
+  int32_t n_shards;
+  int32_t draw;                    /* DSV41_FULL_DRAW_* */
+  const dsv41_full_state* states;  /* [n_shards, rows] */
+  const dsv41_full_pick* picks;    /* [n_shards, rows]; unused for greedy */
+  const float* uniforms;           /* inverse CDF: [rows], checked to lie in [0, 1) */
+  int64_t vocab_size;
+  int64_t* out_ids;                /* [rows] */
+  float* out_logprob;              /* [rows] */
+  int32_t* out_kept;               /* [rows] or NULL */
+  int32_t* out_status;             /* [rows] */
+} dsv41_sampler_full_finish_desc;
 
 /* Finishes a sharded batch from the gathered lists of all slices. */
 typedef struct dsv41_sampler_merge_desc {
@@ -384,6 +453,8 @@ size_t dsv41_logprob_shard_desc_size(void);
 size_t dsv41_logprob_combine_desc_size(void);
 size_t dsv41_sampler_shard_desc_size(void);
 size_t dsv41_sampler_merge_desc_size(void);
+size_t dsv41_sampler_full_shard_desc_size(void);
+size_t dsv41_sampler_full_finish_desc_size(void);
 const char* dsv41_last_error(void);
 
 /* Sampler: replaces rollout.py:144-150 for a [rows, vocab] batch.
@@ -400,6 +471,13 @@ int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t wo
  * the lists are what one all-gather would carry between the two calls. */
 int dsv41_sampler_shard_run(const dsv41_sampler_shard_desc* desc, void* stream /* hipStream_t */);
 int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* desc, void* stream /* hipStream_t */);
+
+/* Vocabulary-sharded full-vocabulary draws: per-slice states, per-slice picks, then the
+ * finish (no workspace).  Together they replace rollout.py:144-148 when the head's
+ * vocabulary is split over GPUs; states and picks are what two all-gathers carry. */
+int dsv41_sampler_full_state_run(const dsv41_sampler_full_shard_desc* desc, void* stream /* hipStream_t */);
+int dsv41_sampler_full_draw_run(const dsv41_sampler_full_shard_desc* desc, void* stream /* hipStream_t */);
+int dsv41_sampler_full_finish_run(const dsv41_sampler_full_finish_desc* desc, void* stream /* hipStream_t */);
 
 /* Fused selected-token log-prob: replaces model.py:679-684 / native_lora.py:80-82. */
 size_t dsv41_logprob_workspace_bytes(const dsv41_logprob_desc* desc);

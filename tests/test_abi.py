@@ -37,7 +37,9 @@ def test_descriptor_layouts_match_header(tmp_path):
               "dsv41_logprob_grad_desc": _lib.LogprobGradDesc, "dsv41_token_tis_desc": _lib.TokenTisDesc,
               "dsv41_grpo_desc": _lib.GrpoDesc,
               "dsv41_logprob_shard_desc": _lib.LogprobShardDesc, "dsv41_logprob_combine_desc": _lib.LogprobCombineDesc,
-              "dsv41_sampler_shard_desc": _lib.SamplerShardDesc, "dsv41_sampler_merge_desc": _lib.SamplerMergeDesc}
+              "dsv41_sampler_shard_desc": _lib.SamplerShardDesc, "dsv41_sampler_merge_desc": _lib.SamplerMergeDesc,
+              "dsv41_sampler_full_shard_desc": _lib.SamplerFullShardDesc,
+              "dsv41_sampler_full_finish_desc": _lib.SamplerFullFinishDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {", 'printf("{");']
     first = True
     for cname, cls in fields.items():
@@ -274,4 +276,59 @@ def test_sampler_merge_rejects_bad_descriptors(kw, code, msg):
     lib = _lib.load()
     d = _merge_desc(**kw)
     assert lib.dsv41_sampler_merge_run(ctypes.byref(d), None) == code
+    assert msg in _lib.last_error()
+
+
+def _full_shard_desc(sampler, **kw):
+    d = _lib.SamplerFullShardDesc()
+    d.struct_size = ctypes.sizeof(_lib.SamplerFullShardDesc)
+    d.sampler = ctypes.pointer(sampler)
+    d.vocab_offset, d.vocab_size = 100, 400
+    d.n_shards, d.shard_index = 3, 1
+    d.states, d.out_states, d.out_picks = 0x7000, 0x8000, 0x9000
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("step,skw,kw,code,msg", [
+    ("state", dict(top_p=0.9), {}, _lib.E_UNSUPPORTED, "no top-k, top-p or min-p"),
+    ("state", dict(top_k=5), {}, _lib.E_UNSUPPORTED, "no top-k, top-p or min-p"),
+    ("state", dict(min_p=0.1), {}, _lib.E_UNSUPPORTED, "no top-k, top-p or min-p"),
+    ("state", {}, dict(vocab_offset=350), _lib.E_INVALID, "within a vocabulary"),
+    ("state", {}, dict(out_states=None), _lib.E_INVALID, "out_states"),
+    ("state", {}, dict(struct_size=8), _lib.E_ABI, "size mismatch"),
+    ("state", dict(replay_ids=0x6000), {}, _lib.E_UNSUPPORTED, "replay_ids"),
+    ("draw", {}, dict(shard_index=3), _lib.E_INVALID, "shard_index"),
+    ("draw", {}, dict(states=None), _lib.E_INVALID, "states and out_picks"),
+    ("draw", dict(uniforms=None), {}, _lib.E_INVALID, "one uniform per row"),
+    ("draw", dict(greedy=1), {}, _lib.E_INVALID, "greedy rows need no draw step"),
+])
+def test_sampler_full_shard_rejects_bad_descriptors(step, skw, kw, code, msg):
+    lib = _lib.load()
+    base = _sampler_desc(out_ids=None, out_logprob=None, out_status=None, **skw)
+    d = _full_shard_desc(base, **kw)
+    run = lib.dsv41_sampler_full_state_run if step == "state" else lib.dsv41_sampler_full_draw_run
+    assert run(ctypes.byref(d), None) == code
+    assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(draw=3), _lib.E_INVALID, "draw must be"),
+    (dict(picks=None), _lib.E_INVALID, "picks"),
+    (dict(uniforms=None), _lib.E_INVALID, "one uniform per row"),
+    (dict(rows=0), _lib.E_INVALID, "must be positive"),
+    (dict(out_ids=None), _lib.E_INVALID, "out_ids"),
+    (dict(struct_size=8), _lib.E_ABI, "size mismatch"),
+])
+def test_sampler_full_finish_rejects_bad_descriptors(kw, code, msg):
+    lib = _lib.load()
+    d = _lib.SamplerFullFinishDesc()
+    d.struct_size = ctypes.sizeof(_lib.SamplerFullFinishDesc)
+    d.rows, d.n_shards, d.draw = 4, 2, _lib.FULL_DRAW_CDF
+    d.states, d.picks, d.uniforms, d.vocab_size = 0x1000, 0x2000, 0x3000, 400
+    d.out_ids, d.out_logprob, d.out_status = 0x4000, 0x5000, 0x6000
+    for k, v in kw.items():
+        setattr(d, k, v)
+    assert lib.dsv41_sampler_full_finish_run(ctypes.byref(d), None) == code
     assert msg in _lib.last_error()

@@ -26,7 +26,7 @@ def run_both(logits, uniforms=None, history=None, history_lens=None, **knobs):
                  history_lens=None if history_lens is None else history_lens.to(DEV),
                  check=False, **knobs)
     torch.cuda.synchronize()
-    ora = oracle.sample(logits.float().numpy(), uniforms=None if uniforms is None else uniforms.numpy(),
+    ora = oracle.sample(logits.float().cpu().numpy(), uniforms=None if uniforms is None else uniforms.cpu().numpy(),
                         history=None if history is None else history.numpy(),
                         history_lens=None if history_lens is None else history_lens.numpy(), **knobs)
     gpu = tuple(t.cpu().numpy() for t in (res.ids, res.logprobs, res.kept, res.status))
@@ -129,6 +129,25 @@ def test_deferred_selection_keeps_min_p_survivors_only():
     kept = gpu[2]
     assert (kept[0::3] == 1).all()
     assert (kept[1::3] > 128).all() and (kept[2::3] > 64).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("knobs", [dict(greedy=True), dict(), dict(top_k=20, top_p=0.9)])
+def test_row_views_ending_inside_a_vector(dtype, knobs):
+    """Rows that are views of a padded vocabulary (16-byte aligned rows whose valid ids end
+    inside a 16-byte vector): the last valid id carries the row maximum and must be read."""
+    g = torch.Generator().manual_seed(51)
+    rows, V, padded = 16, 1001, 1024
+    base = torch.randn(rows, padded, generator=g)
+    base[:, V - 1] = 12.0
+    base[:, V:] = 50.0  # padding past the view: never part of a row
+    x = base.to(dtype).to(DEV)[:, :V]  # the view itself goes to the sampler (16-byte aligned rows)
+    assert x.stride(0) == padded
+    u = torch.rand(rows, generator=g)
+    gpu, ora = run_both(x, None if knobs.get("greedy") else u, None, **knobs)
+    assert_exact(gpu, ora)
+    if knobs.get("greedy"):
+        assert (gpu[0] == V - 1).all()
 
 
 @pytest.mark.parametrize("knobs", [dict(min_p=0.05), dict(min_p=0.1, top_p=0.97), dict(min_p=0.05, greedy=True)])

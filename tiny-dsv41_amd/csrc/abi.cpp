@@ -22,4 +22,6 @@ extern "C" size_t dsv41_logprob_shard_desc_size(void) { return sizeof(dsv41_logp
 extern "C" size_t dsv41_logprob_combine_desc_size(void) { return sizeof(dsv41_logprob_combine_desc); }
 extern "C" size_t dsv41_sampler_shard_desc_size(void) { return sizeof(dsv41_sampler_shard_desc); }
 extern "C" size_t dsv41_sampler_merge_desc_size(void) { return sizeof(dsv41_sampler_merge_desc); }
+extern "C" size_t dsv41_sampler_full_shard_desc_size(void) { return sizeof(dsv41_sampler_full_shard_desc); }
+extern "C" size_t dsv41_sampler_full_finish_desc_size(void) { return sizeof(dsv41_sampler_full_finish_desc); }
 extern "C" const char* dsv41_last_error(void) { return dsv41::g_last_error.c_str(); }

@@ -78,6 +78,10 @@ constexpr int ST_FALLBACK = 1 << 29; // internal: an internal-k TOPK row needs g
 constexpr int DRAW_CDF = 0;     // inverse CDF against one uniform
 constexpr int DRAW_RACE = 1;    // exponential race against Exp(1) variates
 constexpr int DRAW_REPLAY = 2;  // no draw: the log-prob of a given token
+// vocabulary slices of a full-vocabulary draw (dsv41_sampler_full_*_run)
+constexpr int DRAW_STATE = 3;       // the slice's state: max, fixed-order mass, first argmax
+constexpr int DRAW_SHARD_CDF = 4;   // inverse CDF against the gathered states
+constexpr int DRAW_SHARD_RACE = 5;  // exponential race against the gathered states
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -115,6 +119,11 @@ struct Params {
   // cut its min-p survivors at it is flagged ST_FALLBACK and redone by generic_kernel,
   // which then runs only on flagged rows (only_flagged)
   int topk_internal, only_flagged;
+  // full-vocabulary draw over slices (DRAW_STATE / DRAW_SHARD_*): states [n_shards, nrows]
+  const dsv41_full_state* sh_states;
+  dsv41_full_state* sh_out_states;
+  dsv41_full_pick* sh_out_picks;
+  int n_shards, shard_index, nrows;
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -810,6 +819,19 @@ __device__ __forceinline__ void write_result(const Params& p, int row, Misc* m, 
   p.out_status[row] = st;
 }
 
+// A row's maximum and total over the gathered slice states, in slice order (fp64); the
+// draw kernels and the finish kernel evaluate the same expression on the same states.
+__device__ __forceinline__ double slice_weight(const dsv41_full_state& st, float M) {
+  return st.max_z > NEG_INF ? st.mass * exp((double)st.max_z - (double)M) : 0.0;
+}
+__device__ __forceinline__ void combine_states(const dsv41_full_state* states, int n_shards, int nrows, int row,
+                                               float& M, double& S) {
+  M = NEG_INF;
+  for (int s = 0; s < n_shards; ++s) M = fmaxf(M, states[(int64_t)s * nrows + row].max_z);
+  S = 0.0;
+  for (int s = 0; s < n_shards; ++s) S += slice_weight(states[(int64_t)s * nrows + row], M);
+}
+
 __device__ __forceinline__ float row_uniform(const Params& p, int row, Misc* m) {
   if (p.greedy) return 0.0f;
   const float u = p.uniforms[row];
@@ -862,7 +884,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       [&]() {
         if (tid == 0) m->status = 0;
         __syncthreads();
-        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+        if (p.has_pen) U = build_history<NT, HR, (DRAW >= DRAW_STATE)>(p, row, hi, h, m);
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
@@ -952,7 +974,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     return;
   }
 
-  if (DRAW == DRAW_RACE && !p.greedy) {
+  if ((DRAW == DRAW_RACE || DRAW == DRAW_SHARD_RACE) && !p.greedy) {
     // (a separate instantiation: the race's registers would cost the inverse-CDF draw occupancy)
     // Exponential race: the token is argmax_i p_i / E_i with p_i = exp(log_softmax(z)_i),
     // each step in fp32 as torch forms it (log_softmax = z - (max + log(sum)), exp,
@@ -963,8 +985,10 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     __syncthreads();
     float csum = 0.0f;
     for (int c = tid; c < NC; c += NT) csum += cs[c];
-    const double S = (double)block_sum_d<NT>((double)csum, m);
-    const float lsum = M + logf((float)S);
+    double S = (double)block_sum_d<NT>((double)csum, m);
+    float Mr = M;  // the row's maximum (a slice: over all slices)
+    if constexpr (DRAW == DRAW_SHARD_RACE) combine_states(p.sh_states, p.n_shards, p.nrows, row, Mr, S);
+    const float lsum = Mr + logf((float)S);
     const float* erow = p.exps + (int64_t)row * p.estride;
     const __amdgpu_buffer_rsrc_t re = row_rsrc(erow, (uint32_t)p.V * 4u);
     float best = -1.0f;
@@ -1017,6 +1041,25 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
           bi = m->ri[w];
         }
       m->ri[0] = bi;
+      m->rf[0] = b;
+    }
+    if constexpr (DRAW == DRAW_SHARD_RACE) {
+      // this slice's best p / E, its global id and logit; the finish takes the best slice
+      if (tid == 0) {
+        const int bi = m->ri[0];
+        dsv41_full_pick pk;
+        pk.id = -1;
+        pk.z = NEG_INF;
+        pk.ratio = -1.0f;
+        if (bi != 0x7FFFFFFF) {
+          const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
+          pk.id = (int64_t)bi + p.voff;
+          pk.z = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
+          pk.ratio = m->rf[0];
+        }
+        p.sh_out_picks[row] = pk;
+      }
+      return;
     }
     // the log-prob against the fixed-order total, as the other draws report it
     if (wid == 0) {
@@ -1038,13 +1081,41 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   }
 
   // total mass and the chunk holding the draw (wave 0, fp64)
-  const float u = row_uniform(p, row, m);
+  const float u = DRAW == DRAW_STATE ? 0.0f : row_uniform(p, row, m);
+  double t_shard = 0.0;
+  if constexpr (DRAW == DRAW_SHARD_CDF) {
+    // Every slice finds, from the same gathered states, the slice whose share of the total
+    // holds u * S; only that one places the token, against the target in its own units.
+    float Mg;
+    double Sg;
+    combine_states(p.sh_states, p.n_shards, p.nrows, row, Mg, Sg);
+    const double tg = (double)u * Sg;
+    double acc = 0.0, before = 0.0;
+    int owner = -1, last = -1;
+    for (int s = 0; s < p.n_shards; ++s) {
+      const double w = slice_weight(p.sh_states[(int64_t)s * p.nrows + row], Mg);
+      if (w > 0.0) last = s;
+      if (owner < 0 && w > 0.0 && tg < acc + w) {
+        owner = s;
+        before = acc;
+      }
+      acc += w;
+    }
+    const bool past = owner < 0;  // rounding: the last slice with mass takes its last token
+    if (past) owner = last;
+    if (owner != p.shard_index) {  // uniform over the workgroup
+      if (tid == 0) p.sh_out_picks[row] = dsv41_full_pick{-1, NEG_INF, -1.0f};
+      return;
+    }
+    const dsv41_full_state& me = p.sh_states[(int64_t)p.shard_index * p.nrows + row];
+    t_shard = past ? __builtin_huge_val() : (tg - before) * exp((double)Mg - (double)me.max_z);
+  }
   if (wid == 0) {
     const int per = (NC + 63) / 64;
     const int b = lane * per, e = min(b + per, NC);
     double s, incl;
     const double S = chunk_total(incl, s);
-    const double t = (double)u * S;
+    const double t = DRAW == DRAW_SHARD_CDF ? t_shard : (double)u * S;
     double before = incl - s;
     int cstar = -1;
     double cbefore = 0.0;
@@ -1117,7 +1188,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
         }
       }
     };
-    if (p.greedy) {
+    if (p.greedy || DRAW == DRAW_STATE) {  // the state carries the first argmax
       int best = pfirst;
       if (cfirst < NC) {
         float z[G];
@@ -1177,8 +1248,20 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       ztok = zc;
     }
     if (lane == 0) {
-      const float lp = (float)(((double)ztok - (double)M) - log(S));
-      write_result(p, row, m, tok, lp, p.V);
+      if constexpr (DRAW == DRAW_STATE) {
+        dsv41_full_state st;
+        st.max_z = M;
+        st.status = m->status;
+        st.mass = S;
+        st.argmax = tok + p.voff;
+        st.reserved = 0;
+        p.sh_out_states[row] = st;
+      } else if constexpr (DRAW == DRAW_SHARD_CDF) {
+        p.sh_out_picks[row] = dsv41_full_pick{tok + p.voff, ztok, 0.0f};
+      } else {
+        const float lp = (float)(((double)ztok - (double)M) - log(S));
+        write_result(p, row, m, tok, lp, p.V);
+      }
     }
   }
 }
@@ -2509,6 +2592,64 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
   block_final<NT>(p, row, m, cand, n, hist);
 }
 
+// One thread per row of a full-vocabulary draw over slices: the row's maximum and total
+// from the gathered states, the token from the picks (inverse CDF: the one slice that
+// placed it; race: the best p / E, first id on ties; greedy: the first slice holding the
+// maximum), and the outputs as full_kernel writes them.
+__global__ __launch_bounds__(256) void full_finish_kernel(dsv41_sampler_full_finish_desc d) {
+  const int row = blockIdx.x * 256 + (int)threadIdx.x;
+  if (row >= d.rows) return;
+  float M;
+  double S;
+  combine_states(d.states, d.n_shards, d.rows, row, M, S);
+  int st = 0;
+  for (int s = 0; s < d.n_shards; ++s) st |= d.states[(int64_t)s * d.rows + row].status;
+  int64_t tok = 0;
+  float ztok = M;
+  if (d.draw == DSV41_FULL_DRAW_GREEDY) {
+    for (int s = 0; s < d.n_shards; ++s) {
+      const dsv41_full_state& x = d.states[(int64_t)s * d.rows + row];
+      if (M > NEG_INF && x.max_z == M) {
+        tok = x.argmax;
+        break;
+      }
+    }
+  } else if (d.draw == DSV41_FULL_DRAW_RACE) {
+    float best = -1.0f;
+    int64_t bid = INT64_MAX;
+    for (int s = 0; s < d.n_shards; ++s) {
+      const dsv41_full_pick& pk = d.picks[(int64_t)s * d.rows + row];
+      if (pk.id >= 0 && (pk.ratio > best || (pk.ratio == best && pk.id < bid))) {
+        best = pk.ratio;
+        bid = pk.id;
+        ztok = pk.z;
+      }
+    }
+    if (bid != INT64_MAX) tok = bid;
+  } else {
+    const float u = d.uniforms[row];
+    if (!(u >= 0.0f && u < 1.0f)) st |= ST_BAD_UNIFORM;
+    for (int s = 0; s < d.n_shards; ++s) {
+      const dsv41_full_pick& pk = d.picks[(int64_t)s * d.rows + row];
+      if (pk.id >= 0) {
+        tok = pk.id;
+        ztok = pk.z;
+        break;
+      }
+    }
+  }
+  if (st & ST_NONFINITE) {
+    d.out_ids[row] = -1;
+    d.out_logprob[row] = __builtin_nanf("");
+    if (d.out_kept) d.out_kept[row] = 0;
+  } else {
+    d.out_ids[row] = tok;
+    d.out_logprob[row] = (float)(((double)ztok - (double)M) - log(S));
+    if (d.out_kept) d.out_kept[row] = (int32_t)d.vocab_size;
+  }
+  d.out_status[row] = st;
+}
+
 // ====================================================================== host
 template <class K>
 int launch(K kernel, int nt, size_t lds, int rows, const Params& prm, hipStream_t stream) {
@@ -2568,7 +2709,11 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   }
   pl->has_pen = pen_on && hist_given;
   pl->esize = d->logits_dtype == DSV41_DTYPE_F32 ? 4 : 2;
-  pl->vec = ((uintptr_t)d->logits % 16 == 0) && ((d->logits_row_stride * pl->esize) % 16 == 0);
+  // Vector loads also need each row's valid bytes to end on a 16-byte boundary: the buffer
+  // range check zeroes a dword that reaches past the row, so a row ending inside a vector
+  // (a view of a padded vocabulary, a vocabulary slice) would read its last ids as zero.
+  pl->vec = ((uintptr_t)d->logits % 16 == 0) && ((d->logits_row_stride * pl->esize) % 16 == 0) &&
+            (((int64_t)d->vocab * pl->esize) % 16 == 0);
   const int V = d->vocab;
   const bool truncating = d->min_p > 0.0f || (d->top_k > 0 && d->top_k < V) || d->top_p < 1.0f;
   if (d->exponentials && truncating)
@@ -2836,6 +2981,89 @@ extern "C" int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* d, void* 
   DSV41_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(merge_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT));
   hipLaunchKernelGGL(merge_kernel, dim3(d->rows), dim3(TOPK_NT), lds, s, p, in);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
+}
+
+// Checks a slice descriptor of a full-vocabulary draw and returns its Params.
+static int full_shard_params(const dsv41_sampler_full_shard_desc* d, bool draw, Plan* pl, Params* out) {
+  if (!d) return fail(DSV41_E_INVALID, "sampler full shard descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_sampler_full_shard_desc))
+    return fail(DSV41_E_ABI, "dsv41_sampler_full_shard_desc size mismatch (rebuild the binding)");
+  const dsv41_sampler_desc* sd = d->sampler;
+  if (!sd) return fail(DSV41_E_INVALID, "sampler full shard: the slice's sampler descriptor is NULL");
+  int rc = plan(sd, pl, true);
+  if (rc != DSV41_OK) return rc;
+  if (pl->mode != MODE_FULL || sd->top_k != 0)
+    return fail(DSV41_E_UNSUPPORTED, "vocabulary-sharded full-vocabulary draws take no top-k, top-p or min-p");
+  if (sd->replay_ids) return fail(DSV41_E_UNSUPPORTED, "sampler full shard: replay_ids are not sharded");
+  if (d->vocab_offset < 0 || d->vocab_size < d->vocab_offset + sd->vocab || d->vocab_size > MAX_VOCAB)
+    return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of at most 2^21 ids");
+  if (draw) {
+    if (sd->greedy) return fail(DSV41_E_INVALID, "sampler full shard: greedy rows need no draw step (finish from the states)");
+    if (d->n_shards <= 0 || d->shard_index < 0 || d->shard_index >= d->n_shards)
+      return fail(DSV41_E_INVALID, "sampler full shard: shard_index must be in [0, n_shards)");
+    if (!d->states || !d->out_picks)
+      return fail(DSV41_E_INVALID, "sampler full shard: states and out_picks are required");
+    if (!sd->exponentials && !sd->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
+  } else if (!d->out_states) {
+    return fail(DSV41_E_INVALID, "sampler full shard: out_states is required");
+  }
+  Params p = make_params(sd, *pl, nullptr);
+  p.greedy = 0;
+  p.voff = (int)d->vocab_offset;
+  p.vfull = (int)d->vocab_size;
+  p.sh_states = d->states;
+  p.sh_out_states = d->out_states;
+  p.sh_out_picks = d->out_picks;
+  p.n_shards = d->n_shards;
+  p.shard_index = d->shard_index;
+  p.nrows = sd->rows;
+  *out = p;
+  return DSV41_OK;
+}
+
+template <int DRAW>
+static int launch_full(const Plan& pl, int rows, const Params& p, hipStream_t s) {
+  if (pl.esize == 2) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW>, FULL_NT, pl.lds, rows, p, s)
+                                   : launch(full_kernel<uint16_t, 8, false, DRAW>, FULL_NT, pl.lds, rows, p, s);
+  return pl.vec ? launch(full_kernel<float, 4, true, DRAW>, FULL_NT, pl.lds, rows, p, s)
+                : launch(full_kernel<float, 4, false, DRAW>, FULL_NT, pl.lds, rows, p, s);
+}
+
+extern "C" int dsv41_sampler_full_state_run(const dsv41_sampler_full_shard_desc* d, void* stream) {
+  Plan pl;
+  Params p;
+  int rc = full_shard_params(d, false, &pl, &p);
+  if (rc != DSV41_OK) return rc;
+  return launch_full<DRAW_STATE>(pl, d->sampler->rows, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsv41_sampler_full_draw_run(const dsv41_sampler_full_shard_desc* d, void* stream) {
+  Plan pl;
+  Params p;
+  int rc = full_shard_params(d, true, &pl, &p);
+  if (rc != DSV41_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d->sampler->exponentials) return launch_full<DRAW_SHARD_RACE>(pl, d->sampler->rows, p, s);
+  return launch_full<DRAW_SHARD_CDF>(pl, d->sampler->rows, p, s);
+}
+
+extern "C" int dsv41_sampler_full_finish_run(const dsv41_sampler_full_finish_desc* d, void* stream) {
+  if (!d) return fail(DSV41_E_INVALID, "sampler full finish descriptor is NULL");
+  if (d->struct_size != sizeof(dsv41_sampler_full_finish_desc))
+    return fail(DSV41_E_ABI, "dsv41_sampler_full_finish_desc size mismatch (rebuild the binding)");
+  if (d->rows <= 0 || d->n_shards <= 0)
+    return fail(DSV41_E_INVALID, "sampler full finish: rows and n_shards must be positive");
+  if (d->draw != DSV41_FULL_DRAW_CDF && d->draw != DSV41_FULL_DRAW_RACE && d->draw != DSV41_FULL_DRAW_GREEDY)
+    return fail(DSV41_E_INVALID, "sampler full finish: draw must be DSV41_FULL_DRAW_CDF, _RACE or _GREEDY");
+  if (!d->states || (d->draw != DSV41_FULL_DRAW_GREEDY && !d->picks))
+    return fail(DSV41_E_INVALID, "sampler full finish: states (and picks, unless greedy) are required");
+  if (d->draw == DSV41_FULL_DRAW_CDF && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
+  if (!d->out_ids || !d->out_logprob || !d->out_status)
+    return fail(DSV41_E_INVALID, "out_ids, out_logprob and out_status are required");
+  hipLaunchKernelGGL(full_finish_kernel, dim3((d->rows + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     *d);
   DSV41_HIP_CHECK(hipGetLastError());
   return DSV41_OK;
 }

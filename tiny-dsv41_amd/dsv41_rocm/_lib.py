@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).with_name("libdsv41hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -231,6 +231,49 @@ class SamplerMergeDesc(ctypes.Structure):
     ]
 
 
+class SamplerFullShardDesc(ctypes.Structure):
+    """dsv41_sampler_full_shard_desc: one vocabulary slice of a full-vocabulary draw."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("n_shards", ctypes.c_int32),
+        ("sampler", ctypes.POINTER(SamplerDesc)),
+        ("vocab_offset", ctypes.c_int64),
+        ("vocab_size", ctypes.c_int64),
+        ("shard_index", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("states", ctypes.c_void_p),
+        ("out_states", ctypes.c_void_p),
+        ("out_picks", ctypes.c_void_p),
+    ]
+
+
+class SamplerFullFinishDesc(ctypes.Structure):
+    """dsv41_sampler_full_finish_desc: the finish of a full-vocabulary draw over slices."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("rows", ctypes.c_int32),
+        ("n_shards", ctypes.c_int32),
+        ("draw", ctypes.c_int32),
+        ("states", ctypes.c_void_p),
+        ("picks", ctypes.c_void_p),
+        ("uniforms", ctypes.c_void_p),
+        ("vocab_size", ctypes.c_int64),
+        ("out_ids", ctypes.c_void_p),
+        ("out_logprob", ctypes.c_void_p),
+        ("out_kept", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+    ]
+
+
+FULL_DRAW_CDF = 0
+FULL_DRAW_RACE = 1
+FULL_DRAW_GREEDY = 2
+FULL_STATE_BYTES = 32  # dsv41_full_state
+FULL_PICK_BYTES = 16   # dsv41_full_pick
+
+
 EXPORTS = (
     "dsv41_abi_version",
     "dsv41_sampler_desc_size",
@@ -242,6 +285,8 @@ EXPORTS = (
     "dsv41_logprob_combine_desc_size",
     "dsv41_sampler_shard_desc_size",
     "dsv41_sampler_merge_desc_size",
+    "dsv41_sampler_full_shard_desc_size",
+    "dsv41_sampler_full_finish_desc_size",
     "dsv41_last_error",
     "dsv41_sampler_workspace_bytes",
     "dsv41_sampler_run",
@@ -257,6 +302,9 @@ EXPORTS = (
     "dsv41_logprob_combine_run",
     "dsv41_sampler_shard_run",
     "dsv41_sampler_merge_run",
+    "dsv41_sampler_full_state_run",
+    "dsv41_sampler_full_draw_run",
+    "dsv41_sampler_full_finish_run",
 )
 
 _lock = threading.Lock()
@@ -274,6 +322,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_logprob_combine_desc_size.restype = ctypes.c_size_t
     lib.dsv41_sampler_shard_desc_size.restype = ctypes.c_size_t
     lib.dsv41_sampler_merge_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_sampler_full_shard_desc_size.restype = ctypes.c_size_t
+    lib.dsv41_sampler_full_finish_desc_size.restype = ctypes.c_size_t
     lib.dsv41_last_error.restype = ctypes.c_char_p
     lib.dsv41_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.dsv41_sampler_workspace_bytes.argtypes = [ctypes.POINTER(SamplerDesc)]
@@ -307,6 +357,11 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_sampler_shard_run.argtypes = [ctypes.POINTER(SamplerShardDesc), ctypes.c_void_p]
     lib.dsv41_sampler_merge_run.restype = ctypes.c_int
     lib.dsv41_sampler_merge_run.argtypes = [ctypes.POINTER(SamplerMergeDesc), ctypes.c_void_p]
+    for name in ("dsv41_sampler_full_state_run", "dsv41_sampler_full_draw_run"):
+        getattr(lib, name).restype = ctypes.c_int
+        getattr(lib, name).argtypes = [ctypes.POINTER(SamplerFullShardDesc), ctypes.c_void_p]
+    lib.dsv41_sampler_full_finish_run.restype = ctypes.c_int
+    lib.dsv41_sampler_full_finish_run.argtypes = [ctypes.POINTER(SamplerFullFinishDesc), ctypes.c_void_p]
     return lib
 
 
@@ -341,6 +396,10 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("dsv41_sampler_shard_desc layout differs between library and binding")
         if lib.dsv41_sampler_merge_desc_size() != ctypes.sizeof(SamplerMergeDesc):
             raise RuntimeError("dsv41_sampler_merge_desc layout differs between library and binding")
+        if lib.dsv41_sampler_full_shard_desc_size() != ctypes.sizeof(SamplerFullShardDesc):
+            raise RuntimeError("dsv41_sampler_full_shard_desc layout differs between library and binding")
+        if lib.dsv41_sampler_full_finish_desc_size() != ctypes.sizeof(SamplerFullFinishDesc):
+            raise RuntimeError("dsv41_sampler_full_finish_desc layout differs between library and binding")
         _lib = lib
         return lib
 

@@ -330,6 +330,178 @@ def merge_shards(
     return SampleResult(ids, lps, kept, out_status)
 
 
+def full_shard_states(
+    logits: torch.Tensor,
+    *,
+    vocab_offset: int,
+    vocab_size: int,
+    temperature: float = 1.0,
+    history: Optional[torch.Tensor] = None,
+    history_lens: Optional[torch.Tensor] = None,
+    repetition_penalty: float = 1.0,
+    presence_penalty: float = 0.0,
+    frequency_penalty: float = 0.0,
+) -> torch.Tensor:
+    """Step 1 of a full-vocabulary draw (no top-k, top-p or min-p: the reference's training
+    mode, ``rollout.py:144-148``) over a vocabulary-sharded batch.  This GPU's logits cover the
+    ids ``[vocab_offset, vocab_offset + logits.shape[1])`` of a ``vocab_size`` vocabulary and
+    ``history`` holds global ids.  Returns the slice's state per row, int64 ``[rows, 4]`` (the
+    32-byte ``dsv41_full_state``: its largest processed logit, status bits, its mass in a fixed
+    order and its first argmax).  Gather the states of all slices (slices in vocabulary order)
+    for :func:`full_shard_draw` and :func:`full_shard_finish`."""
+    logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
+    rows, width = logits.shape
+    if not (0 <= vocab_offset and vocab_offset + width <= vocab_size):
+        raise ValueError("the slice must lie within the vocabulary")
+    device = logits.device
+    states = torch.empty(rows, _lib.FULL_STATE_BYTES // 8, dtype=torch.int64, device=device)
+    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                      frequency_penalty, 0, 1.0, 0.0)
+    d = _lib.SamplerFullShardDesc()
+    d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullShardDesc)
+    d.sampler = _lib.ctypes.pointer(desc)
+    d.vocab_offset, d.vocab_size = vocab_offset, vocab_size
+    d.out_states = states.data_ptr()
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_full_state_run(_lib.ctypes.byref(d), stream)
+    _lib.check(rc)
+    return states
+
+
+def _gathered(parts, words: int, what: str) -> torch.Tensor:
+    t = torch.stack(list(parts)) if isinstance(parts, (list, tuple)) else parts
+    if t.ndim != 3 or t.shape[2] != words or t.dtype != torch.int64:
+        raise ValueError(f"{what} must be the int64 [n_shards, rows, {words}] gathered from every slice")
+    return t.contiguous()
+
+
+def full_shard_draw(
+    logits: torch.Tensor,
+    states,
+    *,
+    shard_index: int,
+    vocab_offset: int,
+    vocab_size: int,
+    temperature: float = 1.0,
+    uniforms: Optional[torch.Tensor] = None,
+    exponentials: Optional[torch.Tensor] = None,
+    history: Optional[torch.Tensor] = None,
+    history_lens: Optional[torch.Tensor] = None,
+    repetition_penalty: float = 1.0,
+    presence_penalty: float = 0.0,
+    frequency_penalty: float = 0.0,
+) -> torch.Tensor:
+    """Step 2 of a full-vocabulary draw over slices: with every slice's state gathered
+    (``states``: a list in slice order, or int64 ``[n_shards, rows, 4]``), this slice places the
+    token when its share of the row's total holds ``u * S`` (inverse CDF against ``uniforms``,
+    the same fp32 ``[rows]`` on every slice), or reports its best ``p / E`` over its columns
+    (``exponentials``: this slice's columns of the rows' Exp(1) variates, the exponential race
+    that reproduces ``torch.multinomial``).  Returns int64 ``[rows, 2]`` (the 16-byte
+    ``dsv41_full_pick``) for :func:`full_shard_finish`.  Greedy rows need no draw step."""
+    logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
+    rows, width = logits.shape
+    if not (0 <= vocab_offset and vocab_offset + width <= vocab_size):
+        raise ValueError("the slice must lie within the vocabulary")
+    device = logits.device
+    st = _gathered(states, _lib.FULL_STATE_BYTES // 8, "states").to(device)
+    if st.shape[1] != rows:
+        raise ValueError("states must hold one state per row of every slice")
+    if not 0 <= shard_index < st.shape[0]:
+        raise ValueError("shard_index must name one of the gathered slices")
+    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                      frequency_penalty, 0, 1.0, 0.0)
+    if exponentials is not None:
+        exponentials = exponentials.to(device=device, dtype=torch.float32)
+        if exponentials.shape != logits.shape:
+            raise ValueError("exponentials must have the shape of this slice's logits")
+        if exponentials.stride(1) != 1:
+            exponentials = exponentials.contiguous()
+        desc.exponentials = exponentials.data_ptr()
+        desc.exponentials_row_stride = exponentials.stride(0)
+    else:
+        if uniforms is None:
+            raise ValueError("a sharded inverse-CDF draw needs the batch's uniforms on every slice")
+        uniforms = uniforms.to(device=device, dtype=torch.float32).contiguous()
+        if uniforms.shape != (rows,):
+            raise ValueError("one uniform is required per row")
+        desc.uniforms = uniforms.data_ptr()
+    picks = torch.empty(rows, _lib.FULL_PICK_BYTES // 8, dtype=torch.int64, device=device)
+    d = _lib.SamplerFullShardDesc()
+    d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullShardDesc)
+    d.n_shards = st.shape[0]
+    d.sampler = _lib.ctypes.pointer(desc)
+    d.vocab_offset, d.vocab_size = vocab_offset, vocab_size
+    d.shard_index = shard_index
+    d.states = st.data_ptr()
+    d.out_picks = picks.data_ptr()
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_full_draw_run(_lib.ctypes.byref(d), stream)
+    _lib.check(rc)
+    return picks
+
+
+def full_shard_finish(
+    states,
+    picks=None,
+    *,
+    vocab_size: int,
+    draw: str = "inverse_cdf",
+    uniforms: Optional[torch.Tensor] = None,
+    check: bool = True,
+) -> SampleResult:
+    """Step 3 of a full-vocabulary draw over slices: the token from the gathered picks
+    (``draw`` = ``"inverse_cdf"`` or ``"exponential_race"``) or, for ``"greedy"``, from the
+    states alone, and its log-prob ``(z - M) - log S`` against the row's maximum and total.
+    Returns what :func:`sample` returns for the unsharded logits; ``uniforms`` (inverse CDF)
+    are checked and ``check`` raises as there."""
+    modes = {"inverse_cdf": _lib.FULL_DRAW_CDF, "exponential_race": _lib.FULL_DRAW_RACE,
+             "greedy": _lib.FULL_DRAW_GREEDY}
+    if draw not in modes:
+        raise ValueError("draw must be 'inverse_cdf', 'exponential_race' or 'greedy'")
+    st = _gathered(states, _lib.FULL_STATE_BYTES // 8, "states")
+    n_shards, rows, _ = st.shape
+    device = st.device
+    pk = None
+    if draw != "greedy":
+        if picks is None:
+            raise ValueError("the draw's picks from every slice are required")
+        pk = _gathered(picks, _lib.FULL_PICK_BYTES // 8, "picks").to(device)
+        if pk.shape[:2] != (n_shards, rows):
+            raise ValueError("picks must hold one pick per row of every slice")
+    if draw == "inverse_cdf":
+        if uniforms is None:
+            raise ValueError("sampling requires one uniform per row")
+        uniforms = uniforms.to(device=device, dtype=torch.float32).contiguous()
+        if uniforms.shape != (rows,):
+            raise ValueError("one uniform is required per row")
+    ids = torch.empty(rows, dtype=torch.int64, device=device)
+    lps = torch.empty(rows, dtype=torch.float32, device=device)
+    kept = torch.empty(rows, dtype=torch.int32, device=device)
+    status = torch.empty(rows, dtype=torch.int32, device=device)
+    d = _lib.SamplerFullFinishDesc()
+    d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullFinishDesc)
+    d.rows, d.n_shards, d.draw = rows, n_shards, modes[draw]
+    d.states = st.data_ptr()
+    d.picks = _device_ptr(pk)
+    d.uniforms = _device_ptr(uniforms if draw == "inverse_cdf" else None)
+    d.vocab_size = vocab_size
+    d.out_ids, d.out_logprob, d.out_kept, d.out_status = (ids.data_ptr(), lps.data_ptr(), kept.data_ptr(),
+                                                          status.data_ptr())
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.dsv41_sampler_full_finish_run(_lib.ctypes.byref(d), stream)
+    _lib.check(rc)
+    if check:
+        if bool((status != 0).any()):
+            _status_error(status)
+    return SampleResult(ids, lps, kept, status)
+
+
 def replay_log_probs(
     logits: torch.Tensor,
     token_ids: torch.Tensor,
