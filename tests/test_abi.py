@@ -190,6 +190,16 @@ def test_python_entry_points_fail_loudly_off_gpu():
     with pytest.raises(ValueError, match="GPU"):
         selected_log_probs(torch.zeros(3, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
                            torch.zeros(3, dtype=torch.int64))
+    from dsv41_rocm import full_shard_draw, full_shard_finish, full_shard_states
+    with pytest.raises(ValueError, match="GPU"):
+        full_shard_states(torch.zeros(2, 10), vocab_offset=0, vocab_size=10)
+    with pytest.raises(ValueError, match="GPU"):
+        full_shard_draw(torch.zeros(2, 10), torch.zeros(1, 2, 4, dtype=torch.int64), shard_index=0,
+                        vocab_offset=0, vocab_size=10, uniforms=torch.zeros(2))
+    with pytest.raises(ValueError, match="draw must be"):
+        full_shard_finish(torch.zeros(1, 2, 4, dtype=torch.int64), vocab_size=10, draw="top_p")
+    with pytest.raises(ValueError, match=r"\[n_shards, rows, 4\]"):
+        full_shard_finish(torch.zeros(2, 4, dtype=torch.int64), vocab_size=10, draw="greedy")
 
 
 def test_custom_ops_registered_with_fake_kernels():
