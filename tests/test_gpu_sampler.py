@@ -131,6 +131,27 @@ def test_deferred_selection_keeps_min_p_survivors_only():
     assert (kept[1::3] > 128).all() and (kept[2::3] > 64).all()
 
 
+@pytest.mark.parametrize("V,dtype,pen", [
+    (20011, torch.float32, dict(repetition_penalty=1.1)),                          # 256 threads, bitmap only
+    (20011, torch.float32, dict(presence_penalty=0.3, frequency_penalty=0.2)),     # 256 threads, full tables
+    (20011, torch.bfloat16, dict(repetition_penalty=0.9)),                         # 256 threads, raising penalty
+    (151936, torch.float32, dict(repetition_penalty=1.05, frequency_penalty=0.1)), # tables too large: 512 threads
+])
+def test_deferred_batches_on_both_workgroup_sizes(V, dtype, pen):
+    """Top-k batches above 256 rows run 256-thread workgroups when their tables fit four per
+    CU, 512-thread ones otherwise; both hand their candidates to the deferred selection."""
+    g = torch.Generator().manual_seed(61)
+    rows = 288
+    x = (2.0 * torch.randn(rows, V, generator=g)).to(dtype)
+    x[::7] = (0.02 * torch.randn(len(range(0, rows, 7)), V, generator=g)).to(dtype)  # flat rows
+    hist = torch.randint(0, V, (rows, 512), generator=g)
+    hist[:, ::3] = hist[:, :1]  # repeated ids: counts above one
+    u = torch.rand(rows, generator=g)
+    knobs = dict(temperature=0.8, top_k=100, top_p=0.95, min_p=0.02, **pen)
+    gpu, ora = run_both(x, u, hist, **knobs)
+    assert_exact(gpu, ora)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("knobs", [dict(greedy=True), dict(), dict(top_k=20, top_p=0.9)])
 def test_row_views_ending_inside_a_vector(dtype, knobs):

@@ -31,6 +31,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace dsv41 {
@@ -124,6 +126,9 @@ struct Params {
   dsv41_full_state* sh_out_states;
   dsv41_full_pick* sh_out_picks;
   int n_shards, shard_index, nrows;
+  // TOPK with lowering penalties and no frequency penalty needs only the membership
+  // bitmap: ucap is 0 then and the rank table is left out of the layout
+  int no_ranks;
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -159,8 +164,9 @@ __host__ __device__ inline int n_chunks(int V) {
 // LDS layout; must agree between the launch (host) and the kernel (device).
 // bitmap u32[words] | wrank u16[words] | cnt u16[ucap] | tok u32[ucap] |
 // penx f32[ucap] (FULL) | 256 u64 radix bins | chunks (FULL) or candidates (TOPK)
+// ranks = false: the membership bitmap alone (no rank, count or token tables).
 template <int MODE, int G>
-__host__ __device__ inline Layout make_layout(int V, int words, int ucap, int cap) {
+__host__ __device__ inline Layout make_layout(int V, int words, int ucap, int cap, bool ranks = true) {
   Layout l;
   size_t off = 0;
   l.misc = off;
@@ -168,7 +174,7 @@ __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int ca
   l.bitmap = off;
   off += 4 * (size_t)words;
   l.wrank = off;
-  off = align16(off + 2 * (size_t)words);
+  off = align16(off + 2 * (size_t)(ranks ? words : 0));
   l.cnt = off;
   off = align16(off + 2 * (size_t)((ucap + 1) & ~1));
   l.tok = off;
@@ -496,14 +502,16 @@ __device__ __forceinline__ int rank_below(const Hist& h, int e, int words, int U
 
 // History ids of one row, loaded into registers at kernel start so that the table
 // build does not wait on memory twice; ids past HR*NT are read again from memory.
-template <int HR>
+// IdT = int32_t keeps each id in one register: negative ids (padding) become -1 and ids
+// past 2^31 - 1 become INT32_MAX, which every vocabulary check still flags.
+template <int HR, typename IdT = int64_t>
 struct HistIds {
-  int64_t id[HR];
+  IdT id[HR];
   int hl;
 };
 
-template <int NT, int HR>
-__device__ __forceinline__ void load_history(const Params& p, int row, HistIds<HR>& hi) {
+template <int NT, int HR, typename IdT>
+__device__ __forceinline__ void load_history(const Params& p, int row, HistIds<HR, IdT>& hi) {
   hi.hl = 0;
   if (!p.has_pen) return;
   const int tid = threadIdx.x;
@@ -512,7 +520,11 @@ __device__ __forceinline__ void load_history(const Params& p, int row, HistIds<H
 #pragma unroll
   for (int j = 0; j < HR; ++j) {
     const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(tid + j * NT) * 8u, 0, 0);
-    hi.id[j] = (int64_t)(((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x);
+    const int64_t g = (int64_t)(((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x);
+    if constexpr (sizeof(IdT) == 4)
+      hi.id[j] = g < 0 ? -1 : (g > (int64_t)INT32_MAX ? INT32_MAX : (int32_t)g);
+    else
+      hi.id[j] = g;
   }
   int hl = p.hlens ? p.hlens[row] : p.hlen;
   hi.hl = max(0, min(hl, (int)p.hstride));
@@ -520,8 +532,8 @@ __device__ __forceinline__ void load_history(const Params& p, int row, HistIds<H
 
 // Builds the tables; returns the number of slots (distinct in-vocabulary ids).  With
 // counts false only the membership bitmap is built and 0 is returned.
-template <int NT, int HR, bool SHARD = false>
-__device__ __forceinline__ int build_history(const Params& p, int row, const HistIds<HR>& hi, const Hist& h, Misc* m,
+template <int NT, int HR, bool SHARD = false, typename IdT = int64_t>
+__device__ __forceinline__ int build_history(const Params& p, int row, const HistIds<HR, IdT>& hi, const Hist& h, Misc* m,
                                              bool counts = true) {
   // a vocabulary shard keeps the ids of its own range; ids past the whole vocabulary flag the row
   const int64_t id_off = SHARD ? p.voff : 0, id_lim = SHARD ? p.vfull : p.V;
@@ -746,8 +758,8 @@ template <typename T>
 __device__ __forceinline__ void landed(T v) {
   asm volatile("" ::"v"(v));
 }
-template <int HR>
-__device__ __forceinline__ void landed(const HistIds<HR>& hi) {
+template <int HR, typename IdT>
+__device__ __forceinline__ void landed(const HistIds<HR, IdT>& hi) {
 #pragma unroll
   for (int j = 0; j < HR; ++j) landed(hi.id[j]);
 }
@@ -1612,19 +1624,22 @@ __device__ __forceinline__ void block_final(const Params& p, int row, Misc* m, u
 
 // EMIT: the launch covers one vocabulary shard; each row's candidates leave for
 // merge_kernel instead of being sampled here.
-template <typename TIn, bool VEC, bool EMIT = false>
-__global__ __launch_bounds__(TOPK_NT) void topk_kernel(Params p) {
-  constexpr int NT = TOPK_NT, NW = NT / 64, G = TOPK_G, TILE = TOPK_TILE, HR = 8;
+// NTK = 256 (deferred batches whose tables fit four workgroups per CU) holds 16 history ids
+// per thread as int32: 4096 ids in the registers that 8 int64 ids take at NTK = 512.
+template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT>
+__global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
+  constexpr int NT = NTK, NW = NT / 64, G = TOPK_G, TILE = NT * G, HR = 4096 / NT;
+  using IdT = std::conditional_t<(NT < TOPK_NT), int32_t, int64_t>;
   constexpr int NE = PF * G + 1;  // elements per thread in one batch round (+1 history slot)
   extern __shared__ __align__(16) unsigned char smem[];
-  const Layout L = make_layout<MODE_TOPK, G>(p.V, p.words, p.ucap, p.cap);
+  const Layout L = make_layout<MODE_TOPK, G>(p.V, p.words, p.ucap, p.cap, p.no_ranks == 0);
   Misc* m = reinterpret_cast<Misc*>(smem + L.misc);
   const Hist h = hist_tables(smem, L);
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + L.hist256);
   uint64_t* cand = reinterpret_cast<uint64_t*>(smem + L.mode0);
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  HistIds<HR> hi;
+  HistIds<HR, IdT> hi;
   load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
@@ -2671,6 +2686,8 @@ struct Plan {
   int words, ucap, cap;
   size_t lds;
   size_t workspace;
+  int topk_nt;        // TOPK threads per workgroup: TOPK_NT, or 256 (see plan)
+  bool bitmap_only;   // TOPK penalties need only the membership bitmap
 };
 
 // shard: the descriptor describes one vocabulary slice (dsv41_sampler_shard_run); the draw
@@ -2759,6 +2776,23 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   if (pl->lds > LDS_LIMIT)
     return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
   pl->defer = !shard && pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
+  // Deferred TOPK batches whose tables fit four 256-thread workgroups per CU (a quarter of
+  // LDS) run with 256 threads: 128 VGPRs then hold four rows per CU instead of two, so a
+  // row building its history tables leaves three others streaming.  Lowering penalties
+  // without a frequency penalty need only the membership bitmap.
+  pl->topk_nt = TOPK_NT;
+  pl->bitmap_only = pl->has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&
+                    d->frequency_penalty == 0.0f;
+  if (pl->defer) {
+    const int cap256 = k_eff + 256 * TOPK_G;
+    const Layout L256 = make_layout<MODE_TOPK, TOPK_G>(V, pl->words, pl->bitmap_only ? 0 : pl->ucap, cap256,
+                                                       !pl->bitmap_only);
+    if (4 * L256.total <= LDS_LIMIT) {
+      pl->topk_nt = 256;
+      pl->cap = cap256;
+      pl->lds = L256.total;
+    }
+  }
   pl->workspace = 0;
   if (pl->defer) pl->workspace += (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
   if (pl->mode == MODE_GENERIC || pl->mode == MODE_TOPP || pl->internal_k) {
@@ -2889,10 +2923,23 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
       return pl.vec ? launch(full_kernel<float, 4, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
                     : launch(full_kernel<float, 4, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
     case MODE_TOPK: {
-      if (bf) rc = pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
-                          : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
-      else rc = pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
-                       : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
+      if (pl.topk_nt == 256) {
+        Params q = p;
+        if (pl.bitmap_only) {
+          q.ucap = 0;
+          q.no_ranks = 1;
+        }
+        if (bf) rc = pl.vec ? launch(topk_kernel<uint16_t, true, false, 256>, 256, pl.lds, d->rows, q, s)
+                            : launch(topk_kernel<uint16_t, false, false, 256>, 256, pl.lds, d->rows, q, s);
+        else rc = pl.vec ? launch(topk_kernel<float, true, false, 256>, 256, pl.lds, d->rows, q, s)
+                         : launch(topk_kernel<float, false, false, 256>, 256, pl.lds, d->rows, q, s);
+      } else if (bf) {
+        rc = pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
+                    : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
+      } else {
+        rc = pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
+                    : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
+      }
       if (rc != DSV41_OK) return rc;
       if (pl.defer) {
         hipLaunchKernelGGL(select_kernel, dim3((d->rows + SEL_WAVES - 1) / SEL_WAVES), dim3(SEL_WAVES * 64), 0, s,
