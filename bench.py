@@ -36,7 +36,7 @@ BF16_PEAK_TFLOPS = 2500.0
 # counts are in profiles/sampler_topk_E.md, profiles/logprob_fused_D.md and
 # profiles/logprob_backward_D.md.  Workloads without an entry report null.
 MEASURED_TRAFFIC = {
-    "sampler_E": 2_631_736_448 + 2_494_896,  # topk_kernel + select_kernel
+    "sampler_E": 2_629_506_528 + 1_937_544,  # topk_kernel + select_kernel
     "logprob_D": 46_112_195_686 + 1_048_576,
     "logprob_grad_D": 45_297_095_573 + 4_384_320_091,
 }
