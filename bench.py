@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--workload", default="E", choices=["A", "B", "E", "none"],
                     help="sampler config; 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
-    ap.add_argument("--logprob-steps", type=int, default=8)
+    ap.add_argument("--logprob-steps", type=int, default=10)
     ap.add_argument("--no-backward", action="store_true", help="skip the log-prob backward timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -217,7 +217,7 @@ def main():
         line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
         print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
-        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 2, not args.no_cpu_baseline, torch,
+        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 3, not args.no_cpu_baseline, torch,
                                         backward=not args.no_backward)
     print(json.dumps(line), flush=True)
 
