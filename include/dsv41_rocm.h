@@ -58,7 +58,8 @@ extern "C" {
 
 /* Per-row / per-token status bits written to out_status (0 = clean). */
 #define DSV41_STATUS_NONFINITE 1   /* a processed logit / result was NaN or +-inf      */
-#define DSV41_STATUS_BAD_HISTORY 2 /* a history id was >= vocab (id ignored)           */
+#define DSV41_STATUS_BAD_HISTORY 2 /* a history id was >= vocab (id ignored); history  */
+                                   /* is read only when a penalty is active             */
 #define DSV41_STATUS_BAD_UNIFORM 4 /* uniform outside [0, 1) (row drawn with u = 0)    */
 #define DSV41_STATUS_RATIO_ZERO 8  /* Token-TIS raw weight exp(old - behaviour) == 0   */
 #define DSV41_STATUS_BAD_TARGET 16 /* a replay id was outside [0, vocab) (lp = NaN)    */
@@ -461,7 +462,11 @@ const char* dsv41_last_error(void);
  * Workspace (8-byte aligned, contents need no initialisation): rows*vocab*4 bytes for
  * top-p / min-p without top-k (the radix path); rows*(256*8+4) bytes for top-k batches
  * above 256 rows, whose rows hand up to 256 candidate keys and a count to a second
- * kernel on the same stream for the final selection; none otherwise. */
+ * kernel on the same stream for the final selection; S*rows*(top_k*8+8) bytes for a
+ * top-k batch (top_k <= 256) too small to fill the GPU, whose rows are split into S
+ * 2048-aligned vocabulary slices (about 256 workgroups in all, S*top_k <= 4096) that
+ * each leave their local top_k keys, a count and a status for a merge kernel on the
+ * same stream; none otherwise. */
 size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* desc);
 int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream /* hipStream_t */);

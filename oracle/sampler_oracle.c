@@ -143,6 +143,9 @@ int dsv41_oracle_process_row(const float* x, int V, const int64_t* hist, int hle
                              float rp, float pres, float freq, uint32_t* counts, float* z) {
   int status = 0;
   memset(counts, 0, sizeof(uint32_t) * (size_t)V);
+  /* history is read only when a penalty is active: neutral knobs leave every logit as is
+     and flag nothing */
+  if (rp == 1.0f && pres == 0.0f && freq == 0.0f) hlen = 0;
   for (int j = 0; j < hlen; ++j) {
     int64_t id = hist[j];
     if (id < 0) continue;

@@ -152,6 +152,43 @@ def test_deferred_batches_on_both_workgroup_sizes(V, dtype, pen):
     assert_exact(gpu, ora)
 
 
+@pytest.mark.parametrize("rows,V,dtype,knobs", [
+    (1, 151936, torch.float32, dict(top_k=50, top_p=0.95, repetition_penalty=1.1)),        # 75 slices
+    (3, 129281, torch.float32, dict(top_k=256, presence_penalty=0.4, frequency_penalty=0.1)),  # odd V: scalar loads
+    (40, 50000, torch.bfloat16, dict(top_k=7, min_p=0.05, repetition_penalty=0.9)),       # 5 slices, ragged last
+    (100, 151936, torch.bfloat16, dict(top_k=64, top_p=0.9)),                              # 2 slices
+    (100, 151936, torch.float32, dict(top_k=64, repetition_penalty=1.2, greedy=True)),
+])
+def test_small_top_k_batches_sliced_over_the_gpu(rows, V, dtype, knobs):
+    """Top-k batches too small to fill the GPU split each row into vocabulary slices; every
+    slice emits its exact local top_k and a merge finishes the row, with the same kept sets,
+    ids and log-probs as one pass over the row.  Row maxima sit in the last slice, on slice
+    boundaries and in the first; history holds ids past the vocabulary and padding (flagged
+    only where a penalty reads the history)."""
+    g = torch.Generator().manual_seed(71)
+    x = 2.5 * torch.randn(rows, V, generator=g)
+    x[0, V - 1] = 14.0
+    if rows > 1:
+        x[1, 2047:2049] = 13.0  # a tie across the first slice boundary: the lower id wins
+    if rows > 2:
+        x[2, 0] = 13.0
+    x = x.to(dtype)
+    hist = torch.randint(0, V, (rows, 300), generator=g)
+    hist[:, ::11] = -1
+    if rows > 2:
+        hist[2, 5] = V + 3  # flags row 2 only
+    u = torch.rand(rows, generator=g)
+    gpu, ora = run_both(x, None if knobs.get("greedy") else u, hist, **knobs)
+    assert_exact(gpu, ora)
+    k = knobs["top_k"]
+    assert (gpu[2][gpu[3] == 0] <= k).all()
+    pen = any(key.endswith("_penalty") for key in knobs)
+    if rows > 2:  # history is read, and checked, only under an active penalty
+        assert bool(gpu[3][2] & 2) == pen and (np.delete(gpu[3], 2) == 0).all()
+    if knobs.get("greedy"):
+        assert gpu[0][0] == V - 1 and gpu[0][1] == 2047
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("knobs", [dict(greedy=True), dict(), dict(top_k=20, top_p=0.9)])
 def test_row_views_ending_inside_a_vector(dtype, knobs):

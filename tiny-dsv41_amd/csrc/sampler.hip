@@ -126,6 +126,9 @@ struct Params {
   dsv41_full_state* sh_out_states;
   dsv41_full_pick* sh_out_picks;
   int n_shards, shard_index, nrows;
+  // sliced small batch (topk_kernel<..., EMIT, NTK, SLICED>): workgroup b takes slice
+  // b % n_slices (slice_w ids from slice * slice_w) of row b / n_slices
+  int n_slices, slice_w;
   // TOPK with lowering penalties and no frequency penalty needs only the membership
   // bitmap: ucap is 0 then and the rank table is left out of the layout
   int no_ranks;
@@ -1626,8 +1629,21 @@ __device__ __forceinline__ void block_final(const Params& p, int row, Misc* m, u
 // merge_kernel instead of being sampled here.
 // NTK = 256 (deferred batches whose tables fit four workgroups per CU) holds 16 history ids
 // per thread as int32: 4096 ids in the registers that 8 int64 ids take at NTK = 512.
-template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT>
+//
+// SLICED (with EMIT): a batch too small to fill the GPU, spread over it.  Each workgroup
+// emits its slice's exact local top_k, as a vocabulary shard does, into
+// [n_slices, nrows, emit_cap]; merge_kernel then finishes every row exactly.
+template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT, bool SLICED = false>
 __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
+  static_assert(!SLICED || EMIT, "a sliced launch emits candidate lists");
+  const int row = SLICED ? (int)blockIdx.x / p.n_slices : (int)blockIdx.x;
+  const int erow = SLICED ? ((int)blockIdx.x % p.n_slices) * p.nrows + row : row;  // output slot
+  if constexpr (SLICED) {
+    const int v0 = ((int)blockIdx.x % p.n_slices) * p.slice_w;
+    p.voff = v0;
+    p.V = min(p.slice_w, p.vfull - v0);
+    p.logits = reinterpret_cast<const TIn*>(p.logits) + v0;
+  }
   constexpr int NT = NTK, NW = NT / 64, G = TOPK_G, TILE = NT * G, HR = 4096 / NT;
   using IdT = std::conditional_t<(NT < TOPK_NT), int32_t, int64_t>;
   constexpr int NE = PF * G + 1;  // elements per thread in one batch round (+1 history slot)
@@ -1638,7 +1654,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + L.hist256);
   uint64_t* cand = reinterpret_cast<uint64_t*>(smem + L.mode0);
 
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   HistIds<HR, IdT> hi;
   load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
@@ -1925,14 +1941,14 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
       for (int i = tid; i < count; i += NT) el += minp_ok(ckey_z(cand[i]), zmax, p) ? 1 : 0;
       keep = min(p.top_k, block_sum_i<NT>(el, m));
     }
-    uint64_t* out = p.emit_keys + (int64_t)row * p.emit_cap;
+    uint64_t* out = p.emit_keys + (int64_t)erow * p.emit_cap;
     for (int i = tid; i < keep; i += NT) {
       const uint64_t k = cand[i];
       out[i] = ckey(ckey_z(k), ckey_idx(k) + (uint32_t)p.voff);
     }
     if (tid == 0) {
-      p.emit_count[row] = keep;
-      p.out_status[row] = m->status;
+      p.emit_count[erow] = keep;
+      p.out_status[erow] = m->status;
     }
     return;
   }
@@ -2688,6 +2704,10 @@ struct Plan {
   size_t workspace;
   int topk_nt;        // TOPK threads per workgroup: TOPK_NT, or 256 (see plan)
   bool bitmap_only;   // TOPK penalties need only the membership bitmap
+  // sliced small TOPK batch (slices > 1): slice width, its table sizes and LDS, the merge's
+  // LDS, and the workspace offsets of the slices' keys, counts and statuses
+  int slices, slice_w, slice_words, slice_ucap;
+  size_t slice_lds, merge_lds, ws_counts, ws_status;
 };
 
 // shard: the descriptor describes one vocabulary slice (dsv41_sampler_shard_run); the draw
@@ -2795,6 +2815,34 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   }
   pl->workspace = 0;
   if (pl->defer) pl->workspace += (size_t)d->rows * (DEFER_KEYS * sizeof(uint64_t) + sizeof(int32_t));
+  // A top-k batch too small to fill the GPU (no deferral, no internal bound) is spread over
+  // it: about 256 workgroups, each one tile-aligned slice of a row emitting its exact local
+  // top_k, then the merge.  The union of the slices' lists holds each row's kept set.
+  pl->slices = 1;
+  if (!shard && pl->mode == MODE_TOPK && !pl->defer && !pl->internal_k && d->top_k <= 256) {
+    // the merge holds at most 4096 candidates per row
+    const int want = std::min(std::max(1, 256 / d->rows), 4096 / std::max(1, d->top_k));
+    const int sw = (int)((((int64_t)V + want - 1) / want + TOPK_TILE - 1) / TOPK_TILE * TOPK_TILE);
+    const int S = (V + sw - 1) / sw;
+    if (S >= 2) {
+      const int sw_words = pl->has_pen ? (sw + 31) / 32 : 0;
+      const int sw_ucap = pl->has_pen ? (int)std::min<int64_t>(d->history_row_stride, sw) : 0;
+      const Layout Ls = make_layout<MODE_TOPK, TOPK_G>(sw, sw_words, sw_ucap, d->top_k + TOPK_TILE);
+      const size_t mlds = align16(sizeof(Misc)) + (256 + (size_t)S * d->top_k + (size_t)d->top_k) * sizeof(uint64_t);
+      if (Ls.total <= LDS_LIMIT && mlds <= LDS_LIMIT) {
+        pl->slices = S;
+        pl->slice_w = sw;
+        pl->slice_words = sw_words;
+        pl->slice_ucap = sw_ucap;
+        pl->slice_lds = Ls.total;
+        pl->merge_lds = mlds;
+        const size_t n = (size_t)S * d->rows;
+        pl->ws_counts = n * d->top_k * sizeof(uint64_t);
+        pl->ws_status = pl->ws_counts + n * sizeof(int32_t);
+        pl->workspace = pl->ws_status + n * sizeof(int32_t);
+      }
+    }
+  }
   if (pl->mode == MODE_GENERIC || pl->mode == MODE_TOPP || pl->internal_k) {
     pl->workspace = align16(pl->workspace);  // the z rows follow the hand-over area
     pl->workspace += (size_t)d->rows * (size_t)V * sizeof(float);
@@ -2877,6 +2925,48 @@ extern "C" size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* d) {
   return pl.workspace;
 }
 
+// A small top-k batch spread over the GPU: each (row, slice) workgroup emits its exact
+// local top_k into the workspace, then merge_kernel finishes every row.
+static int run_sliced(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, char* ws, hipStream_t s) {
+  Params q = p;
+  q.words = pl.slice_words;
+  q.ucap = pl.slice_ucap;
+  q.cap = d->top_k + TOPK_TILE;
+  q.voff = 0;
+  q.vfull = d->vocab;
+  q.n_slices = pl.slices;
+  q.slice_w = pl.slice_w;
+  q.nrows = d->rows;
+  q.emit_cap = d->top_k;
+  q.emit_keys = reinterpret_cast<uint64_t*>(ws);
+  q.emit_count = reinterpret_cast<int32_t*>(ws + pl.ws_counts);
+  q.out_status = reinterpret_cast<int32_t*>(ws + pl.ws_status);
+  const int grid = d->rows * pl.slices;
+  int rc;
+  if (pl.esize == 2) rc = pl.vec ? launch(topk_kernel<uint16_t, true, true, TOPK_NT, true>, TOPK_NT, pl.slice_lds, grid, q, s)
+                                 : launch(topk_kernel<uint16_t, false, true, TOPK_NT, true>, TOPK_NT, pl.slice_lds, grid, q, s);
+  else rc = pl.vec ? launch(topk_kernel<float, true, true, TOPK_NT, true>, TOPK_NT, pl.slice_lds, grid, q, s)
+                   : launch(topk_kernel<float, false, true, TOPK_NT, true>, TOPK_NT, pl.slice_lds, grid, q, s);
+  if (rc != DSV41_OK) return rc;
+  Params m{};
+  m.uniforms = d->uniforms;
+  m.out_ids = d->out_ids;
+  m.out_lp = d->out_logprob;
+  m.out_kept = d->out_kept;
+  m.out_status = d->out_status;
+  m.log_min_p = p.log_min_p;
+  m.min_p = d->min_p;
+  m.top_p = d->top_p;
+  m.top_k = d->top_k;
+  m.greedy = d->greedy ? 1 : 0;
+  MergeIn in{q.emit_keys, q.emit_count, q.out_status, pl.slices, d->rows, d->top_k, d->top_k};
+  DSV41_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(merge_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT));
+  hipLaunchKernelGGL(merge_kernel, dim3(d->rows), dim3(TOPK_NT), pl.merge_lds, s, m, in);
+  DSV41_HIP_CHECK(hipGetLastError());
+  return DSV41_OK;
+}
+
 // Rows flagged ST_FALLBACK by topk_kernel (more min-p survivors than the internal bound)
 // or topp_kernel (a boundary bin above TOPP_CAP) again, with generic_kernel; every other
 // row returns at once.
@@ -2923,6 +3013,7 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
       return pl.vec ? launch(full_kernel<float, 4, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
                     : launch(full_kernel<float, 4, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
     case MODE_TOPK: {
+      if (pl.slices > 1) return run_sliced(d, pl, p, static_cast<char*>(workspace), s);
       if (pl.topk_nt == 256) {
         Params q = p;
         if (pl.bitmap_only) {
