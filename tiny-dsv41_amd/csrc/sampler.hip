@@ -2602,7 +2602,7 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
     m->count = n;
   }
   __syncthreads();
-  const int n = m->count;
+  int n = m->count;
   int base = 0;
   for (int s = 0; s < in.shards; ++s) {
     const int c = min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
@@ -2611,6 +2611,18 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
     base += c;
   }
   __syncthreads();
+  // More keys than one wave sorts: keep the union's top_k within the min-p bound of its
+  // largest key, as topk_kernel's own compaction does (every list holds its slice's
+  // largest key, so that bound is the row's).  The final selection is the same on the
+  // survivors, and the one-wave path then takes any top_k up to 256.
+  if (n > 4 * 64) {
+    float zl = NEG_INF;
+    for (int i = tid; i < n; i += NT) zl = fmaxf(zl, ckey_z(cand[i]));
+    const float mz = block_max<NT>(zl, m);
+    float tau = NEG_INF;
+    uint64_t tau_key = 0;
+    n = topk_compact<NT>(cand, n, m, p, mz, tau, tau_key, hist);
+  }
   if (n >= 1 && n <= 4 * 64) {
     if (wid == 0) {
       const float u = row_uniform(p, row, m);
