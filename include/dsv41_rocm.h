@@ -464,7 +464,8 @@ const char* dsv41_last_error(void);
  * above 256 rows, whose rows hand up to 256 candidate keys and a count to a second
  * kernel on the same stream for the final selection; S*rows*(top_k*8+8) bytes for a
  * top-k batch (top_k <= 256) too small to fill the GPU, whose rows are split into S
- * 2048-aligned vocabulary slices (about 256 workgroups in all, S*top_k <= 4096) that
+ * 2048-aligned vocabulary slices of at least 6144 ids (up to about 256 workgroups in
+ * all, S*top_k <= 4096) that
  * each leave their local top_k keys, a count and a status for a merge kernel on the
  * same stream; none otherwise. */
 size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* desc);

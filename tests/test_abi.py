@@ -111,11 +111,12 @@ def test_sampler_workspace_for_the_radix_path_and_deferred_selection():
     assert lib.dsv41_sampler_run(ctypes.byref(big), None, 0, None) == _lib.E_WORKSPACE
     assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(top_k=5, rows=256))) == 0
     assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(_sampler_desc(rows=300))) == 0
-    # a small top-k batch over a long vocabulary is split into 2048-aligned slices (about 256
-    # workgroups, at most 4096 candidates per row): 8 rows x 129280 ids -> 32 slices of 4096
-    # ids, each (slice, row) leaving top_k keys, a count and a status
+    # a small top-k batch over a long vocabulary is split into 2048-aligned slices of at
+    # least 6144 ids (up to about 256 workgroups, at most 4096 candidates per row): 8 rows x
+    # 129280 ids -> 22 slices of 6144 ids, each (slice, row) leaving top_k keys, a count and
+    # a status
     small = _sampler_desc(top_k=50, rows=8, vocab=129280, logits_row_stride=129280)
-    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(small)) == 32 * 8 * (50 * 8 + 4 + 4)
+    assert lib.dsv41_sampler_workspace_bytes(ctypes.byref(small)) == 22 * 8 * (50 * 8 + 4 + 4)
     assert lib.dsv41_sampler_run(ctypes.byref(small), None, 0, None) == _lib.E_WORKSPACE
     # top_k 256 caps the slices at 4096 // 256 = 16
     wide = _sampler_desc(top_k=256, rows=8, vocab=129280, logits_row_stride=129280)

@@ -153,7 +153,7 @@ def test_deferred_batches_on_both_workgroup_sizes(V, dtype, pen):
 
 
 @pytest.mark.parametrize("rows,V,dtype,knobs", [
-    (1, 151936, torch.float32, dict(top_k=50, top_p=0.95, repetition_penalty=1.1)),        # 75 slices
+    (1, 151936, torch.float32, dict(top_k=50, top_p=0.95, repetition_penalty=1.1)),        # 25 slices
     (3, 129281, torch.float32, dict(top_k=256, presence_penalty=0.4, frequency_penalty=0.1)),  # odd V: scalar loads
     (40, 50000, torch.bfloat16, dict(top_k=7, min_p=0.05, repetition_penalty=0.9)),       # 5 slices, ragged last
     (100, 151936, torch.bfloat16, dict(top_k=64, top_p=0.9)),                              # 2 slices

@@ -2832,9 +2832,13 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   // top_k, then the merge.  The union of the slices' lists holds each row's kept set.
   pl->slices = 1;
   if (!shard && pl->mode == MODE_TOPK && !pl->defer && !pl->internal_k && d->top_k <= 256) {
-    // the merge holds at most 4096 candidates per row
+    // the merge holds at most 4096 candidates per row.  A slice spans at least three
+    // tiles: a slice's first tile fills the buffer before any threshold exists, so two
+    // compactions of about 2048 keys come with every slice, and on one or two tiles they
+    // outweigh the stream (measured: 4096-id slices slower than 6144-id ones)
     const int want = std::min(std::max(1, 256 / d->rows), 4096 / std::max(1, d->top_k));
-    const int sw = (int)((((int64_t)V + want - 1) / want + TOPK_TILE - 1) / TOPK_TILE * TOPK_TILE);
+    const int sw = std::max(3 * TOPK_TILE,
+                            (int)((((int64_t)V + want - 1) / want + TOPK_TILE - 1) / TOPK_TILE * TOPK_TILE));
     const int S = (V + sw - 1) / sw;
     if (S >= 2) {
       const int sw_words = pl->has_pen ? (sw + 31) / 32 : 0;
