@@ -189,6 +189,28 @@ def test_small_top_k_batches_sliced_over_the_gpu(rows, V, dtype, knobs):
         assert gpu[0][0] == V - 1 and gpu[0][1] == 2047
 
 
+@pytest.mark.parametrize("greedy", [False, True])
+def test_sliced_batch_statuses(greedy):
+    """Statuses of a sliced top-k batch are the OR of its slices': a NaN and a +inf in late
+    slices, a history id past the vocabulary, and a uniform outside [0, 1); clean rows stay
+    exact next to them."""
+    g = torch.Generator().manual_seed(83)
+    rows, V = 6, 40000  # 7 slices of 6144 ids per row
+    logits = 2.0 * torch.randn(rows, V, generator=g)
+    logits[1, 39000] = float("nan")
+    logits[2, 20000] = float("inf")
+    hist = torch.randint(0, V, (rows, 64), generator=g)
+    hist[3, 7] = V + 11
+    u = torch.rand(rows, generator=g)
+    u[4] = 1.5
+    gpu, ora = run_both(logits, None if greedy else u, hist, greedy=greedy, top_k=10, repetition_penalty=1.1)
+    np.testing.assert_array_equal(gpu[3], ora[3])
+    assert gpu[3][1] & 1 and gpu[3][2] & 1 and gpu[3][3] & 2
+    assert bool(gpu[3][4] & 4) == (not greedy)
+    assert gpu[3][0] == 0 and gpu[3][5] == 0
+    assert_exact(gpu, ora)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("knobs", [dict(greedy=True), dict(), dict(top_k=20, top_p=0.9)])
 def test_row_views_ending_inside_a_vector(dtype, knobs):
