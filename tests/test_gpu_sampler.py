@@ -168,8 +168,10 @@ def test_small_top_k_batches_sliced_over_the_gpu(rows, V, dtype, knobs):
     g = torch.Generator().manual_seed(71)
     x = 2.5 * torch.randn(rows, V, generator=g)
     x[0, V - 1] = 14.0
-    if rows > 1:
-        x[1, 2047:2049] = 13.0  # a tie across the first slice boundary: the lower id wins
+    if rows > 1:  # tied pairs across every 2048-aligned id (each slice boundary among them):
+        b = torch.arange(2048, V, 2048)  # the lowest ids win, whichever slices hold them
+        x[1, b - 1] = 13.0
+        x[1, b] = 13.0
     if rows > 2:
         x[2, 0] = 13.0
     x = x.to(dtype)
