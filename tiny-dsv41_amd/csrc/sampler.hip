@@ -2592,25 +2592,54 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + align16(sizeof(Misc)));
   uint64_t* cand = hist + 256;
   const int row = blockIdx.x, tid = threadIdx.x, wid = tid >> 6;
-  if (tid == 0) {
-    int st = 0, n = 0;
-    for (int s = 0; s < in.shards; ++s) {
-      st |= in.status[(int64_t)s * in.rows + row];
-      n += min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
+  if (in.shards <= 256) {
+    // every list's count and status at once, their offsets in LDS (hist is free until the
+    // compaction), then one flat copy with all loads in flight
+    int* cnt = reinterpret_cast<int*>(hist);
+    int* off = cnt + 256;
+    if (tid == 0) m->status = 0;
+    __syncthreads();
+    if (tid < in.shards) {
+      cnt[tid] = min(max(in.counts[(int64_t)tid * in.rows + row], 0), in.take);
+      const int st = in.status[(int64_t)tid * in.rows + row];
+      if (st) atomicOr(&m->status, st);
     }
-    m->status = st;
-    m->count = n;
+    __syncthreads();
+    if (tid == 0) {
+      int a = 0;
+      for (int s = 0; s < in.shards; ++s) {
+        off[s] = a;
+        a += cnt[s];
+      }
+      m->count = a;
+    }
+    __syncthreads();
+    const int tot = in.shards * in.take;
+    for (int j = tid; j < tot; j += NT) {
+      const int s = j / in.take, i = j - s * in.take;
+      if (i < cnt[s]) cand[off[s] + i] = in.keys[((int64_t)s * in.rows + row) * in.stride + i];
+    }
+  } else {
+    if (tid == 0) {
+      int st = 0, n = 0;
+      for (int s = 0; s < in.shards; ++s) {
+        st |= in.status[(int64_t)s * in.rows + row];
+        n += min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
+      }
+      m->status = st;
+      m->count = n;
+    }
+    __syncthreads();
+    int base = 0;
+    for (int s = 0; s < in.shards; ++s) {
+      const int c = min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
+      const uint64_t* src = in.keys + ((int64_t)s * in.rows + row) * in.stride;
+      for (int i = tid; i < c; i += NT) cand[base + i] = src[i];
+      base += c;
+    }
   }
   __syncthreads();
   int n = m->count;
-  int base = 0;
-  for (int s = 0; s < in.shards; ++s) {
-    const int c = min(max(in.counts[(int64_t)s * in.rows + row], 0), in.take);
-    const uint64_t* src = in.keys + ((int64_t)s * in.rows + row) * in.stride;
-    for (int i = tid; i < c; i += NT) cand[base + i] = src[i];
-    base += c;
-  }
-  __syncthreads();
   // More keys than one wave sorts: keep the union's top_k within the min-p bound of its
   // largest key, as topk_kernel's own compaction does (every list holds its slice's
   // largest key, so that bound is the row's).  The final selection is the same on the
