@@ -146,9 +146,10 @@ def logits_grad(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tenso
 
 
 # Largest bf16 logit-gradient block the backward materialises at once (bytes); the
-# vocabulary is processed in ranges that fit.  At 16384 tokens x 129280 rows one range of
-# 4.2 GB covers the whole head.
-GRAD_BLOCK_BYTES = 8 << 30
+# vocabulary is processed in ranges that fit.  1 GiB is about the fp32 logits of one
+# 2048-token chunk of the reference's scoring head (native_lora.py:76-77: 2048 x 129280 x 4 B
+# = 1.06 GB); at 16384 tokens x 129280 rows it takes four ranges of 32768 rows.
+GRAD_BLOCK_BYTES = 1 << 30
 
 
 def selected_log_probs_backward(hidden, weight, targets, temperature, lse, entropy, grad_logprob,

@@ -136,7 +136,10 @@ def sample(
     (int32 [rows]) optionally gives ragged lengths.  ``uniforms`` (fp32 [rows] in [0, 1))
     drive the draw; when omitted they are drawn with ``torch.rand(rows, generator=generator)``
     on the CPU.  With ``check`` the call synchronises and raises the reference's
-    ``ValueError`` for non-finite rows, out-of-vocabulary history or bad uniforms.
+    ``ValueError`` for non-finite rows, bad uniforms, or a history id at or above the
+    vocabulary size; history is read only when a penalty is active (repetition != 1,
+    presence or frequency != 0), so with neutral penalties such an id is ignored and not
+    flagged.
 
     ``exponentials`` (fp32 ``[rows, vocab]`` of Exp(1) variates) switches the draw to the
     exponential race ``argmax(p / E)``, which is what ``torch.multinomial(p, 1)`` computes on
