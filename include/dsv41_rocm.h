@@ -472,6 +472,21 @@ size_t dsv41_sampler_workspace_bytes(const dsv41_sampler_desc* desc);
 int dsv41_sampler_run(const dsv41_sampler_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream /* hipStream_t */);
 
+/* Sampler without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  It runs dsv41_sampler_run's kernels with the workspace taken
+ * from a static device array of DSV41_SAMPLER_STATIC_SCRATCH_BYTES per GPU (held by every GPU
+ * the library runs on until the process ends) and calls no allocator.  A batch whose
+ * dsv41_sampler_workspace_bytes exceeds that size returns DSV41_E_UNSUPPORTED before any
+ * launch (4096 rows of top-k need 8.4 MB; the radix path's rows*vocab*4 bytes fit only small
+ * batches).  The stream must belong to the current device; the first call on a device looks
+ * up the array's address there, so make it outside graph capture.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller.  Nothing in the array needs clearing between
+ * calls: each launch writes what it later reads. */
+#define DSV41_SAMPLER_STATIC_SCRATCH_BYTES (32u << 20)
+int dsv41_sampler_run_static(const dsv41_sampler_desc* desc, void* stream /* hipStream_t */);
+
 /* Vocabulary-sharded sampler: per-slice candidate lists, then the exact merge (no workspace).
  * Together they replace rollout.py:144-150 when the head's vocabulary is split over GPUs;
  * the lists are what one all-gather would carry between the two calls. */

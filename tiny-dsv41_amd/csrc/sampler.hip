@@ -31,6 +31,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "common.h"
@@ -3029,13 +3031,9 @@ static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params
                 : launch(generic_kernel<float, 4, false>, GEN_NT, lds, d->rows, g, s);
 }
 
-extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
-  Plan pl;
-  int rc = plan(d, &pl);
-  if (rc != DSV41_OK) return rc;
-  if (pl.workspace && (!workspace || workspace_bytes < pl.workspace))
-    return fail(DSV41_E_WORKSPACE, "sampler workspace is missing or too small");
+// The launches of one planned batch; `workspace` holds at least pl.workspace bytes.
+static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* workspace, void* stream) {
+  int rc;
   Params p = make_params(d, pl, workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = pl.esize == 2;
@@ -3098,6 +3096,65 @@ extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, s
       return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, pl.lds, d->rows, p, s)
                     : launch(generic_kernel<float, 4, false>, GEN_NT, pl.lds, d->rows, p, s);
   }
+}
+
+extern "C" int dsv41_sampler_run(const dsv41_sampler_desc* d, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  Plan pl;
+  const int rc = plan(d, &pl);
+  if (rc != DSV41_OK) return rc;
+  if (pl.workspace && (!workspace || workspace_bytes < pl.workspace))
+    return fail(DSV41_E_WORKSPACE, "sampler workspace is missing or too small");
+  return run_planned(d, pl, workspace, stream);
+}
+
+// ------------------------------------------------------------ static scratch
+// The workspace of dsv41_sampler_run_static: one array per GPU, part of the code object's
+// device memory, held until the process ends.  On the host `scratch` names a stand-in, not
+// a device address: host code uses the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[DSV41_SAMPLER_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES];
+
+// The scratch address on the current device, looked up once per device (with that device
+// current).  The stream must belong to the current device.
+int scratch_address(hipStream_t s, void** out) {
+  int dev = 0;
+  DSV41_HIP_CHECK(hipGetDevice(&dev));
+  if (s) {
+    hipDevice_t sdev = 0;
+    DSV41_HIP_CHECK(hipStreamGetDevice(s, &sdev));
+    if ((int)sdev != dev) return fail(DSV41_E_INVALID, "the stream must belong to the current device");
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(DSV41_E_UNSUPPORTED, "device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    DSV41_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail(DSV41_E_HIP, "hipGetSymbolAddress returned no address for the sampler scratch");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DSV41_OK;
+}
+}  // namespace
+
+extern "C" int dsv41_sampler_run_static(const dsv41_sampler_desc* d, void* stream) {
+  Plan pl;
+  int rc = plan(d, &pl);
+  if (rc != DSV41_OK) return rc;
+  if (pl.workspace > (size_t)DSV41_SAMPLER_STATIC_SCRATCH_BYTES)
+    return fail(DSV41_E_UNSUPPORTED, "this batch needs " + std::to_string(pl.workspace) +
+                                         " bytes of scratch, above the static maximum of " +
+                                         std::to_string((size_t)DSV41_SAMPLER_STATIC_SCRATCH_BYTES) +
+                                         " (use dsv41_sampler_run with a workspace)");
+  void* ws = nullptr;
+  rc = scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (rc != DSV41_OK) return rc;
+  return run_planned(d, pl, ws, stream);
 }
 
 extern "C" int dsv41_sampler_shard_run(const dsv41_sampler_shard_desc* d, void* stream) {

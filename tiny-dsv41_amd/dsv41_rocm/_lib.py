@@ -270,6 +270,7 @@ class SamplerFullFinishDesc(ctypes.Structure):
 FULL_DRAW_CDF = 0
 FULL_DRAW_RACE = 1
 FULL_DRAW_GREEDY = 2
+SAMPLER_STATIC_SCRATCH_BYTES = 32 << 20  # DSV41_SAMPLER_STATIC_SCRATCH_BYTES
 FULL_STATE_BYTES = 32  # dsv41_full_state
 FULL_PICK_BYTES = 16   # dsv41_full_pick
 
@@ -290,6 +291,7 @@ EXPORTS = (
     "dsv41_last_error",
     "dsv41_sampler_workspace_bytes",
     "dsv41_sampler_run",
+    "dsv41_sampler_run_static",
     "dsv41_logprob_workspace_bytes",
     "dsv41_logprob_run",
     "dsv41_logprob_grad_run",
@@ -330,6 +332,8 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_sampler_run.restype = ctypes.c_int
     lib.dsv41_sampler_run.argtypes = [ctypes.POINTER(SamplerDesc), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p]
+    lib.dsv41_sampler_run_static.restype = ctypes.c_int
+    lib.dsv41_sampler_run_static.argtypes = [ctypes.POINTER(SamplerDesc), ctypes.c_void_p]
     lib.dsv41_logprob_workspace_bytes.restype = ctypes.c_size_t
     lib.dsv41_logprob_workspace_bytes.argtypes = [ctypes.POINTER(LogprobDesc)]
     lib.dsv41_logprob_run.restype = ctypes.c_int
