@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DSV41_ABI_VERSION 4
+#define DSV41_ABI_VERSION 5
 
 /* Element types of logits / activations. */
 #define DSV41_DTYPE_F32 0
@@ -74,7 +74,9 @@ extern "C" {
  *   top-k  (top_k > 0): keep the first top_k of the survivors in (z desc, index asc);
  *   top-p  (top_p < 1): keep the shortest prefix of that order whose 2^-43 fixed-point
  *                       mass reaches ceil(top_p * total);
- *   draw: inverse CDF in vocabulary order over the kept set against uniforms[r]
+ *   draw: inverse CDF in vocabulary order over the kept set against uniforms[r], on the
+ *         2^-43 fixed-point masses floor(2^43 exp(z_i - z_max)): the first token whose
+ *         cumulative mass exceeds (total * floor(u * 2^32)) >> 32, exact in integers
  *         (greedy != 0: first index of max z instead);
  *   out_logprob = z_tok - log(sum_kept exp(z)), out_kept = kept-set size.
  * history[r * history_row_stride + j], j < (history_lens ? history_lens[r] : hist_len);
@@ -143,20 +145,25 @@ typedef struct dsv41_sampler_shard_desc {
 } dsv41_sampler_shard_desc;
 
 /*
- * Full-vocabulary draws (no top-k, top-p or min-p) over vocabulary slices, in three steps
- * with one all-gather after each of the first two:
+ * Full-vocabulary draws (no top-k, top-p or min-p) over vocabulary slices, in steps with one
+ * all-gather after each:
  *   1. dsv41_sampler_full_state_run: each slice streams its columns once (penalties from the
  *      global history ids, then / T) and writes one dsv41_full_state per row;
- *   2. with the states of all slices gathered ([n_shards, rows], slices in vocabulary
- *      order), dsv41_sampler_full_draw_run forms the row's maximum M and total
- *      S = sum_s mass_s * exp(max_z_s - M) in slice order (fp64).  Inverse CDF: the slice
- *      whose share of S holds u * S re-reads its columns and picks the token; the other
- *      slices report none.  Exponential race: every slice reports its best p / E over its
- *      columns with p = exp(z - (M + log S)) in fp32, first id on ties;
- *   3. with the picks gathered, dsv41_sampler_full_finish_run writes ids, log-probs
- *      lp = (z_tok - M) - log S, kept = vocab_size and status bits, as dsv41_sampler_run
+ *   2. inverse CDF only: with the states of all slices gathered ([n_shards, rows], slices in
+ *      vocabulary order), dsv41_sampler_full_mass_run forms the row's maximum M and writes
+ *      the slice's exact fixed-point mass sum_i floor(2^43 exp(z_i - M)) (u64) per row;
+ *   3. dsv41_sampler_full_draw_run, with the states (and for the inverse CDF the masses)
+ *      gathered.  Inverse CDF: the target is (S * floor(u * 2^32)) >> 32 over the integer
+ *      total S of the masses; the slice whose masses hold it re-reads its columns and picks
+ *      the token exactly as dsv41_sampler_run would, the others report none.  Exponential
+ *      race: every slice reports its best p / E over its columns with
+ *      p = exp(z - (M + log S')) in fp32, S' = sum_s mass_s * exp(max_z_s - M) over the
+ *      states in slice order (fp64), first id on ties;
+ *   4. with the picks gathered, dsv41_sampler_full_finish_run writes ids, log-probs
+ *      lp = (z_tok - M) - log S', kept = vocab_size and status bits, as dsv41_sampler_run
  *      does (greedy needs only the states: the first slice holding M gives its argmax).
- * The states (32 bytes) and picks (16 bytes) per row and slice are the wire format.
+ * The states (32 bytes), masses (8 bytes) and picks (16 bytes) per row and slice are the
+ * wire format.
  */
 typedef struct dsv41_full_state {
   float max_z;      /* the slice's largest processed logit; -inf when it has none */
@@ -183,9 +190,11 @@ typedef struct dsv41_sampler_full_shard_desc {
   int64_t vocab_size;                /* the whole vocabulary; larger history ids flag the row */
   int32_t shard_index;               /* draw step: this slice's position in `states` */
   int32_t reserved;
-  const dsv41_full_state* states;    /* draw step: [n_shards, rows], gathered */
+  const dsv41_full_state* states;    /* mass and draw steps: [n_shards, rows], gathered */
   dsv41_full_state* out_states;      /* state step: [rows] */
   dsv41_full_pick* out_picks;        /* draw step: [rows] */
+  const uint64_t* masses;            /* inverse-CDF draw step: [n_shards, rows], gathered */
+  uint64_t* out_masses;              /* mass step: [rows] */
 } dsv41_sampler_full_shard_desc;
 
 #define DSV41_FULL_DRAW_CDF 0     /* inverse CDF against uniforms */
@@ -493,10 +502,12 @@ int dsv41_sampler_run_static(const dsv41_sampler_desc* desc, void* stream /* hip
 int dsv41_sampler_shard_run(const dsv41_sampler_shard_desc* desc, void* stream /* hipStream_t */);
 int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* desc, void* stream /* hipStream_t */);
 
-/* Vocabulary-sharded full-vocabulary draws: per-slice states, per-slice picks, then the
- * finish (no workspace).  Together they replace rollout.py:144-148 when the head's
- * vocabulary is split over GPUs; states and picks are what two all-gathers carry. */
+/* Vocabulary-sharded full-vocabulary draws: per-slice states, exact masses (inverse CDF
+ * only), per-slice picks, then the finish (no workspace).  Together they replace
+ * rollout.py:144-148 when the head's vocabulary is split over GPUs; states, masses and picks
+ * are what the all-gathers carry. */
 int dsv41_sampler_full_state_run(const dsv41_sampler_full_shard_desc* desc, void* stream /* hipStream_t */);
+int dsv41_sampler_full_mass_run(const dsv41_sampler_full_shard_desc* desc, void* stream /* hipStream_t */);
 int dsv41_sampler_full_draw_run(const dsv41_sampler_full_shard_desc* desc, void* stream /* hipStream_t */);
 int dsv41_sampler_full_finish_run(const dsv41_sampler_full_finish_desc* desc, void* stream /* hipStream_t */);
 

@@ -203,9 +203,12 @@ def test_python_entry_points_fail_loudly_off_gpu():
     with pytest.raises(ValueError, match="GPU"):
         selected_log_probs(torch.zeros(3, 8, dtype=torch.bfloat16), torch.zeros(5, 8, dtype=torch.bfloat16),
                            torch.zeros(3, dtype=torch.int64))
-    from dsv41_rocm import full_shard_draw, full_shard_finish, full_shard_states
+    from dsv41_rocm import full_shard_draw, full_shard_finish, full_shard_masses, full_shard_states
     with pytest.raises(ValueError, match="GPU"):
         full_shard_states(torch.zeros(2, 10), vocab_offset=0, vocab_size=10)
+    with pytest.raises(ValueError, match="GPU"):
+        full_shard_masses(torch.zeros(2, 10), torch.zeros(1, 2, 4, dtype=torch.int64), shard_index=0,
+                          vocab_offset=0, vocab_size=10)
     with pytest.raises(ValueError, match="GPU"):
         full_shard_draw(torch.zeros(2, 10), torch.zeros(1, 2, 4, dtype=torch.int64), shard_index=0,
                         vocab_offset=0, vocab_size=10, uniforms=torch.zeros(2))
@@ -309,6 +312,7 @@ def _full_shard_desc(sampler, **kw):
     d.vocab_offset, d.vocab_size = 100, 400
     d.n_shards, d.shard_index = 3, 1
     d.states, d.out_states, d.out_picks = 0x7000, 0x8000, 0x9000
+    d.masses, d.out_masses = 0xA000, 0xB000
     for k, v in kw.items():
         setattr(d, k, v)
     return d
@@ -323,15 +327,23 @@ def _full_shard_desc(sampler, **kw):
     ("state", {}, dict(struct_size=8), _lib.E_ABI, "size mismatch"),
     ("state", dict(replay_ids=0x6000), {}, _lib.E_UNSUPPORTED, "replay_ids"),
     ("draw", {}, dict(shard_index=3), _lib.E_INVALID, "shard_index"),
-    ("draw", {}, dict(states=None), _lib.E_INVALID, "states and out_picks"),
+    ("draw", {}, dict(states=None), _lib.E_INVALID, "gathered states"),
+    ("draw", {}, dict(out_picks=None), _lib.E_INVALID, "out_picks"),
+    ("draw", {}, dict(masses=None), _lib.E_INVALID, "gathered masses"),
     ("draw", dict(uniforms=None), {}, _lib.E_INVALID, "one uniform per row"),
     ("draw", dict(greedy=1), {}, _lib.E_INVALID, "greedy rows need no draw step"),
+    ("mass", {}, dict(out_masses=None), _lib.E_INVALID, "out_masses"),
+    ("mass", {}, dict(states=None), _lib.E_INVALID, "gathered states"),
+    ("mass", {}, dict(shard_index=-1), _lib.E_INVALID, "shard_index"),
+    ("mass", dict(greedy=1), {}, _lib.E_INVALID, "greedy rows need no draw step"),
+    ("mass", dict(top_k=3), {}, _lib.E_UNSUPPORTED, "no top-k, top-p or min-p"),
 ])
 def test_sampler_full_shard_rejects_bad_descriptors(step, skw, kw, code, msg):
     lib = _lib.load()
     base = _sampler_desc(out_ids=None, out_logprob=None, out_status=None, **skw)
     d = _full_shard_desc(base, **kw)
-    run = lib.dsv41_sampler_full_state_run if step == "state" else lib.dsv41_sampler_full_draw_run
+    run = {"state": lib.dsv41_sampler_full_state_run, "mass": lib.dsv41_sampler_full_mass_run,
+           "draw": lib.dsv41_sampler_full_draw_run}[step]
     assert run(ctypes.byref(d), None) == code
     assert msg in _lib.last_error()
 

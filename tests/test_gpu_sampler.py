@@ -1,8 +1,7 @@
 """GPU parity of the row sampler (libdsv41hip.so through the C ABI) against the C oracle.
 
-Bars: kept sets and greedy / truncated-mode ids bit-exact; full-vocab ids agree on at
-least 99.9% of rows (float inverse CDF vs the oracle's exact fixed-point draw); log-probs
-within 1e-4 absolute (fp32).
+Bars: kept sets and ids bit-exact in every mode (the full-vocabulary inverse CDF draws on
+the same exact fixed-point masses as the oracle); log-probs within 1e-4 absolute (fp32).
 """
 
 import numpy as np
@@ -59,14 +58,37 @@ def test_config_a_greedy_pass():
 def test_config_b_full_vocab_bf16():
     inp = workloads.sampler_inputs("B")
     gpu, ora = run_both(inp["logits"], inp["uniforms"], inp["history"], **inp["knobs"])
-    gids, glp, gkept, gst = gpu
-    oids, olp, okept, ost = ora
-    np.testing.assert_array_equal(gst, ost)
-    assert (gkept == inp["logits"].shape[1]).all()
-    agree = np.mean(gids == oids)
-    assert agree >= 0.999, agree
-    same = gids == oids
-    assert np.max(np.abs(glp[same] - olp[same])) <= LP_TOL
+    assert_exact(gpu, ora)
+    assert (gpu[2] == inp["logits"].shape[1]).all()
+
+
+def oracle_threaded(logits, uniforms, history, knobs, parts=16):
+    """The C oracle over row blocks in threads (ctypes releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    rows = logits.shape[0]
+    cuts = np.linspace(0, rows, parts + 1).astype(int)
+    with ThreadPoolExecutor(parts) as ex:
+        outs = list(ex.map(lambda ab: oracle.sample(logits[ab[0]:ab[1]], uniforms=uniforms[ab[0]:ab[1]],
+                                                     history=history[ab[0]:ab[1]], **knobs),
+                           zip(cuts[:-1], cuts[1:])))
+    return tuple(np.concatenate([o[i] for o in outs]) for i in range(4))
+
+
+@pytest.mark.parametrize("seed,where", [(1, "cpu"), (2, "cpu"), (3, "gpu"), (4, "gpu")])
+def test_config_b_full_vocab_ids_exact_over_many_rows(seed, where):
+    """2048 rows of the B distribution per seed, 8192 over the four seeds, generated on the
+    CPU and on the GPU: every id equals the oracle's.  The earlier float-CDF draw missed about
+    one row in 700 here (a target within rounding distance of a CDF step)."""
+    inp = workloads.sampler_inputs("B", rows=2048, device=DEV if where == "gpu" else "cpu", seed=seed)
+    x, u, h, knobs = inp["logits"], inp["uniforms"], inp["history"], inp["knobs"]
+    print(f"case: B distribution 2048 rows seed={seed} generated on {where}", flush=True)
+    res = sample(x.to(DEV), uniforms=u.to(DEV), history=h.to(DEV), check=False, **knobs)
+    torch.cuda.synchronize()
+    gpu = tuple(t.cpu().numpy() for t in (res.ids, res.logprobs, res.kept, res.status))
+    ora = oracle_threaded(x.float().cpu().numpy(), u.cpu().numpy(), h.cpu().numpy(), knobs)
+    assert_exact(gpu, ora)
+    assert (ora[3] == 0).all()
 
 
 def test_config_b_greedy_is_first_argmax():
@@ -318,11 +340,7 @@ def test_small_and_ragged_vocab(V, mode):
     knobs = dict(full={}, topk=dict(top_k=max(1, V // 2)), topp=dict(top_p=0.8),
                  greedy=dict(greedy=True))[mode]
     gpu, ora = run_both(logits, None if mode == "greedy" else u, **knobs, temperature=0.9)
-    if mode == "full":
-        np.testing.assert_array_equal(gpu[3], ora[3])
-        assert np.mean(gpu[0] == ora[0]) >= 0.8  # 5 rows: float vs exact draw
-    else:
-        assert_exact(gpu, ora)
+    assert_exact(gpu, ora)
 
 
 def test_unaligned_row_stride_and_bf16_topk():

@@ -10,8 +10,10 @@
 // One workgroup per row streams the row from HBM exactly once, through raw buffer
 // loads (out-of-range lanes read 0, so the pipeline has no branches around loads),
 // double-buffered in batches of PF tiles:
-//   FULL    (no truncation): per-chunk (max, sum exp) in LDS, float inverse CDF over
-//           chunk sums, then one 64*G-element chunk is re-read to place the draw.
+//   FULL    (no truncation): per-chunk (max, sum exp) in LDS for the row maximum and the
+//           log-prob's total; an inverse-CDF draw streams the row once more for each
+//           chunk's exact fixed-point mass, then re-reads one 64*G-element chunk to place
+//           the token.
 //   TOPK    (1 <= top_k <= 2048): elements above a running threshold (top-k of what
 //           has been seen, and the min-p bound of the running maximum) go to an LDS
 //           candidate buffer; after the pass the buffer is sorted and every decision
@@ -86,6 +88,7 @@ constexpr int DRAW_REPLAY = 2;  // no draw: the log-prob of a given token
 constexpr int DRAW_STATE = 3;       // the slice's state: max, fixed-order mass, first argmax
 constexpr int DRAW_SHARD_CDF = 4;   // inverse CDF against the gathered states
 constexpr int DRAW_SHARD_RACE = 5;  // exponential race against the gathered states
+constexpr int DRAW_SHARD_MASS = 6;  // the slice's exact fixed-point mass against the gathered maximum
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -127,6 +130,8 @@ struct Params {
   const dsv41_full_state* sh_states;
   dsv41_full_state* sh_out_states;
   dsv41_full_pick* sh_out_picks;
+  const uint64_t* sh_masses;  // [n_shards, nrows] gathered exact masses (DRAW_SHARD_CDF)
+  uint64_t* sh_out_masses;    // [nrows] (DRAW_SHARD_MASS)
   int n_shards, shard_index, nrows;
   // sliced small batch (topk_kernel<..., EMIT, NTK, SLICED>): workgroup b takes slice
   // b % n_slices (slice_w ids from slice * slice_w) of row b / n_slices
@@ -168,7 +173,8 @@ __host__ __device__ inline int n_chunks(int V) {
 
 // LDS layout; must agree between the launch (host) and the kernel (device).
 // bitmap u32[words] | wrank u16[words] | cnt u16[ucap] | tok u32[ucap] |
-// penx f32[ucap] (FULL) | 256 u64 radix bins | chunks (FULL) or candidates (TOPK)
+// penx f32[ucap] (FULL) | 256 u64 radix bins | chunks (FULL: f32 max[NC], f32 sum[NC],
+// u64 exact mass[NC]) or candidates (TOPK)
 // ranks = false: the membership bitmap alone (no rank, count or token tables).
 template <int MODE, int G>
 __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int cap, bool ranks = true) {
@@ -189,7 +195,7 @@ __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int ca
   l.hist256 = off;
   off += 256 * 8;
   l.mode0 = off;
-  if (MODE == MODE_FULL) off += 8 * (size_t)n_chunks<G>(V);
+  if (MODE == MODE_FULL) off += 16 * (size_t)n_chunks<G>(V);  // max, sum (fp32), exact mass (u64)
   if (MODE == MODE_TOPK) off += 8 * (size_t)cap;
   if (MODE == MODE_TOPP) off += 8 * ((size_t)TOPP_BINS + (size_t)n_chunks<G>(V) + (size_t)cap);
   l.total = align16(off);
@@ -226,8 +232,41 @@ __device__ __forceinline__ double exp_det(double d) {
   return p * __longlong_as_double(e << 52);
 }
 
+// floor(2^43 exp_det(z - M)) as an (exact, integer-valued) double.  The same operations as
+// exp_det, arranged for the vector unit: the range checks become a clamp and one select,
+// and the scale by 2^n and by 2^43 is one ldexp with a 32-bit exponent.  Every step is
+// exact except the ones exp_det rounds identically, so the floor is the spec's bit for bit.
+__device__ __forceinline__ double mass_f(float z, double M) {
+  double d = (double)z - M;
+  const bool ok = d >= -40.0;  // false for NaN
+  d = fmin(fmax(d, -40.0), 0.0);
+  const double log2e = 1.4426950408889634074;
+  const double ln2_hi = 6.93147180369123816490e-01;
+  const double ln2_lo = 1.90821492927058770002e-10;
+  const double n = __builtin_rint(d * log2e);
+  double r = __builtin_fma(-n, ln2_hi, d);
+  r = __builtin_fma(-n, ln2_lo, r);
+  double p = 1.0 / 6227020800.0;
+  p = __builtin_fma(p, r, 1.0 / 479001600.0);
+  p = __builtin_fma(p, r, 1.0 / 39916800.0);
+  p = __builtin_fma(p, r, 1.0 / 3628800.0);
+  p = __builtin_fma(p, r, 1.0 / 362880.0);
+  p = __builtin_fma(p, r, 1.0 / 40320.0);
+  p = __builtin_fma(p, r, 1.0 / 5040.0);
+  p = __builtin_fma(p, r, 1.0 / 720.0);
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const double f = __builtin_floor(__builtin_ldexp(p, (int)n + 43));
+  return ok ? f : 0.0;
+}
+
+// Fixed-point mass of a token: floor(2^43 * exp_det(z - zmax)).
 __device__ __forceinline__ uint64_t mass_of(float z, float zmax) {
-  return (uint64_t)(exp_det((double)z - (double)zmax) * 8796093022208.0);  // 2^43
+  return (uint64_t)mass_f(z, (double)zmax);
 }
 
 __device__ __forceinline__ uint64_t top_p_threshold(float p, uint64_t s) {
@@ -1097,79 +1136,115 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     return;
   }
 
-  // total mass and the chunk holding the draw (wave 0, fp64)
-  const float u = DRAW == DRAW_STATE ? 0.0f : row_uniform(p, row, m);
-  double t_shard = 0.0;
-  if constexpr (DRAW == DRAW_SHARD_CDF) {
-    // Every slice finds, from the same gathered states, the slice whose share of the total
-    // holds u * S; only that one places the token, against the target in its own units.
-    float Mg;
+  // Inverse-CDF draws use 2^-43 fixed-point masses q_i = floor(2^43 exp_det(z_i - Mref))
+  // against the row's maximum Mref (a slice: the maximum over all slices), as the oracle and
+  // the truncating kernels do.  Integer sums are associative, so the drawn id does not depend
+  // on the order of any reduction.  A second pass over the row sums each chunk's masses into
+  // cq; the token's place inside its chunk comes from the masses of one more read of that
+  // chunk.  The log-prob keeps the fp32 chunk total above, which every full-vocabulary draw
+  // and the replay share.
+  constexpr bool SHARDED = DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_MASS;
+  const bool exact = SHARDED || (DRAW == DRAW_CDF && !p.greedy);
+  const float u = (DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF) ? row_uniform(p, row, m) : 0.0f;
+  uint64_t* cq = reinterpret_cast<uint64_t*>(smem + L.mode0 + 8 * (size_t)NC);
+  float Mref = M;
+  uint64_t tq = 0;  // the draw's target in this workgroup's masses
+  if constexpr (SHARDED) {
     double Sg;
-    combine_states(p.sh_states, p.n_shards, p.nrows, row, Mg, Sg);
-    const double tg = (double)u * Sg;
-    double acc = 0.0, before = 0.0;
-    int owner = -1, last = -1;
+    combine_states(p.sh_states, p.n_shards, p.nrows, row, Mref, Sg);
+  }
+  if constexpr (DRAW == DRAW_SHARD_CDF) {
+    // Every slice finds, from the same gathered masses, the slice whose masses hold the
+    // target; only that one places the token, against the target less the masses before it.
+    uint64_t S = 0;
+    for (int s = 0; s < p.n_shards; ++s) S += p.sh_masses[(int64_t)s * p.nrows + row];
+    const uint64_t t = draw_target(u, S);
+    uint64_t acc = 0;
+    int owner = -1;
     for (int s = 0; s < p.n_shards; ++s) {
-      const double w = slice_weight(p.sh_states[(int64_t)s * p.nrows + row], Mg);
-      if (w > 0.0) last = s;
-      if (owner < 0 && w > 0.0 && tg < acc + w) {
+      const uint64_t q = p.sh_masses[(int64_t)s * p.nrows + row];
+      if (owner < 0 && t < acc + q) {
         owner = s;
-        before = acc;
+        tq = t - acc;
       }
-      acc += w;
+      acc += q;
     }
-    const bool past = owner < 0;  // rounding: the last slice with mass takes its last token
-    if (past) owner = last;
     if (owner != p.shard_index) {  // uniform over the workgroup
       if (tid == 0) p.sh_out_picks[row] = dsv41_full_pick{-1, NEG_INF, -1.0f};
       return;
     }
-    const dsv41_full_state& me = p.sh_states[(int64_t)p.shard_index * p.nrows + row];
-    t_shard = past ? __builtin_huge_val() : (tg - before) * exp((double)Mg - (double)me.max_z);
+  }
+  if (exact) {
+    const int nt = (p.V + TILE - 1) / TILE;
+    const double Md = (double)Mref;
+    Raw<TIn, G> R0, R1;
+    load_group<TIn, G, VEC>(R0, rs, tid * G);
+    for (int t = 0; t < nt; ++t) {
+      load_group<TIn, G, VEC>(R1, rs, (t + 1) * TILE + tid * G);  // past the row: zeros
+      const int base = t * TILE + tid * G;
+      float x[G], z[G];
+      unpack(R0, x);
+      int dummy = 0;
+      make_z<G, true>(x, base, p, h.bitmap, z, dummy);  // history tokens and the tail read -inf
+      // the G masses are integers of at most 2^43: their sum is exact in fp64
+      double qd = 0.0;
+#pragma unroll
+      for (int j = 0; j < G; ++j) qd += mass_f(z[j], Md);
+      uint64_t q = (uint64_t)qd;
+      q = wave_sum_u64(q);
+      const int c = t * NW + wid;
+      if (lane == 0 && c < NC) cq[c] = q;
+      R0 = R1;
+    }
+    __syncthreads();
+    for (int s = tid; s < U; s += NT)
+      atomicAdd(reinterpret_cast<unsigned long long*>(&cq[h.tok[s] / (64 * G)]),
+                (unsigned long long)mass_of(penz[s], Mref));
+    __syncthreads();
+  }
+  if constexpr (DRAW == DRAW_SHARD_MASS) {
+    // this slice's exact mass against the gathered maximum; the draw step gathers them
+    if (wid == 0) {
+      uint64_t s = 0;
+      for (int c = lane; c < NC; c += 64) s += cq[c];
+      s = wave_sum_u64(s);
+      if (lane == 0) p.sh_out_masses[row] = s;
+    }
+    return;
   }
   if (wid == 0) {
-    const int per = (NC + 63) / 64;
-    const int b = lane * per, e = min(b + per, NC);
-    double s, incl;
-    const double S = chunk_total(incl, s);
-    const double t = DRAW == DRAW_SHARD_CDF ? t_shard : (double)u * S;
-    double before = incl - s;
-    int cstar = -1;
-    double cbefore = 0.0;
-    if (before <= t && t < incl) {
-      int lastpos = -1;
-      for (int c = b; c < e; ++c) {
-        if (cs[c] > 0.0f) lastpos = c;
-        if (t < before + (double)cs[c]) {
-          cstar = c;
-          cbefore = before;
-          break;
+    double own, incl;
+    const double S = chunk_total(incl, own);  // the log-prob's total
+    if (exact) {
+      // the chunk holding the target: lane l sums a contiguous run of chunks, then a scan
+      const int per = (NC + 63) / 64;
+      const int b = lane * per, e = min(b + per, NC);
+      uint64_t s = 0;
+      for (int c = b; c < e; ++c) s += cq[c];
+      const uint64_t qincl = wave_incl_scan_u64(s, lane);
+      if constexpr (DRAW == DRAW_CDF) tq = draw_target(u, __shfl(qincl, 63));
+      int cstar = -1;
+      uint64_t need = 0;
+      uint64_t before = qincl - s;
+      if (before <= tq && tq < qincl) {
+        for (int c = b; c < e; ++c) {
+          if (tq < before + cq[c]) {
+            cstar = c;
+            need = tq - before;
+            break;
+          }
+          before += cq[c];
         }
-        before += (double)cs[c];
       }
-      if (cstar < 0 && lastpos >= 0) {  // rounding: last positive chunk, last element
-        cstar = lastpos;
-        cbefore = t + 1.0;
+      const unsigned long long hit = __ballot(cstar >= 0);
+      if (hit) {
+        const int src_lane = __ffsll((long long)hit) - 1;
+        cstar = __shfl(cstar, src_lane);
+        need = __shfl(need, src_lane);
       }
-    }
-    const unsigned long long hit = __ballot(cstar >= 0);
-    if (hit == 0) {
-      int last = -1;
-      for (int c = b; c < e; ++c)
-        if (cs[c] > 0.0f) last = c;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o));
       if (lane == 0) {
-        m->bi[0] = last;
-        m->bd[0] = -1.0;  // take the last positive element of that chunk
-      }
-    } else {
-      const int src_lane = __ffsll((long long)hit) - 1;
-      cstar = __shfl(cstar, src_lane);
-      cbefore = __shfl(cbefore, src_lane);
-      if (lane == 0) {
-        m->bi[0] = cstar;
-        m->bd[0] = t - cbefore;
+        m->bi[0] = cstar;  // -1: no mass at all (a row without a finite maximum)
+        m->bu[0] = need;
       }
     }
     if (lane == 0) m->bd[1] = S;
@@ -1220,50 +1295,39 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       }
       tok = best;
       ztok = M;
-    } else if (m->bi[0] < 0) {
-      // no chunk carries mass: only rows without a finite maximum (flagged non-finite)
-      tok = 0;
-      ztok = M;
-    } else {
+    } else if (m->bi[0] >= 0) {
+      // the first token of the chunk whose cumulative mass exceeds what the chunk owes
       const int cstar = m->bi[0];
-      const double need = m->bd[0];
+      const uint64_t need = m->bu[0];
       const int base = cstar * 64 * G + lane * G;
-      float z[G], e[G];
+      float z[G];
       chunk_z(cstar, z);
-      double ls = 0.0;
+      uint64_t q[G];
+      uint64_t ls = 0;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        e[j] = exp2f((z[j] - M) * LOG2E);
-        ls += (double)e[j];
+        q[j] = mass_of(z[j], Mref);
+        ls += q[j];
       }
-      const double incl = wave_incl_scan_d(ls, lane);
-      double acc = incl - ls;
+      uint64_t acc = wave_incl_scan_u64(ls, lane) - ls;
       int pick = -1;
-      int lastpos = -1;
+      float zp = NEG_INF;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        if (e[j] > 0.0f) lastpos = base + j;
-        if (pick < 0 && need >= 0.0 && need < acc + (double)e[j] && e[j] > 0.0f) pick = base + j;
-        acc += (double)e[j];
+        if (pick < 0 && need < acc + q[j]) {
+          pick = base + j;
+          zp = z[j];
+        }
+        acc += q[j];
       }
       const unsigned long long hit = __ballot(pick >= 0);
-      int chosen;
       if (hit) {
-        chosen = __shfl(pick, __ffsll((long long)hit) - 1);
-      } else {
-        int lp = lastpos;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) lp = max(lp, __shfl_xor(lp, o));
-        chosen = lp;
+        const int src_lane = __ffsll((long long)hit) - 1;
+        tok = __shfl(pick, src_lane);
+        ztok = __shfl(zp, src_lane);
       }
-      float zc = NEG_INF;
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-        if (base + j == chosen) zc = z[j];
-      zc = wave_max(zc);
-      tok = chosen < 0 ? 0 : chosen;
-      ztok = zc;
     }
+    // else: no mass at all, only rows without a finite maximum (flagged non-finite)
     if (lane == 0) {
       if constexpr (DRAW == DRAW_STATE) {
         dsv41_full_state st;
@@ -3226,7 +3290,8 @@ extern "C" int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* d, void* 
 }
 
 // Checks a slice descriptor of a full-vocabulary draw and returns its Params.
-static int full_shard_params(const dsv41_sampler_full_shard_desc* d, bool draw, Plan* pl, Params* out) {
+// step: 0 = state, 1 = exact mass, 2 = draw
+static int full_shard_params(const dsv41_sampler_full_shard_desc* d, int step, Plan* pl, Params* out) {
   if (!d) return fail(DSV41_E_INVALID, "sampler full shard descriptor is NULL");
   if (d->struct_size != sizeof(dsv41_sampler_full_shard_desc))
     return fail(DSV41_E_ABI, "dsv41_sampler_full_shard_desc size mismatch (rebuild the binding)");
@@ -3239,15 +3304,23 @@ static int full_shard_params(const dsv41_sampler_full_shard_desc* d, bool draw, 
   if (sd->replay_ids) return fail(DSV41_E_UNSUPPORTED, "sampler full shard: replay_ids are not sharded");
   if (d->vocab_offset < 0 || d->vocab_size < d->vocab_offset + sd->vocab || d->vocab_size > MAX_VOCAB)
     return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of at most 2^21 ids");
-  if (draw) {
+  if (step > 0) {
     if (sd->greedy) return fail(DSV41_E_INVALID, "sampler full shard: greedy rows need no draw step (finish from the states)");
     if (d->n_shards <= 0 || d->shard_index < 0 || d->shard_index >= d->n_shards)
       return fail(DSV41_E_INVALID, "sampler full shard: shard_index must be in [0, n_shards)");
-    if (!d->states || !d->out_picks)
-      return fail(DSV41_E_INVALID, "sampler full shard: states and out_picks are required");
+    if (!d->states) return fail(DSV41_E_INVALID, "sampler full shard: the gathered states are required");
+  }
+  if (step == 0 && !d->out_states) return fail(DSV41_E_INVALID, "sampler full shard: out_states is required");
+  if (step == 1) {
+    if (sd->exponentials)
+      return fail(DSV41_E_INVALID, "sampler full shard: the exponential race needs no mass step");
+    if (!d->out_masses) return fail(DSV41_E_INVALID, "sampler full shard: out_masses is required");
+  }
+  if (step == 2) {
+    if (!d->out_picks) return fail(DSV41_E_INVALID, "sampler full shard: out_picks is required");
     if (!sd->exponentials && !sd->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
-  } else if (!d->out_states) {
-    return fail(DSV41_E_INVALID, "sampler full shard: out_states is required");
+    if (!sd->exponentials && !d->masses)
+      return fail(DSV41_E_INVALID, "sampler full shard: an inverse-CDF draw needs the gathered masses");
   }
   Params p = make_params(sd, *pl, nullptr);
   p.greedy = 0;
@@ -3256,6 +3329,8 @@ static int full_shard_params(const dsv41_sampler_full_shard_desc* d, bool draw, 
   p.sh_states = d->states;
   p.sh_out_states = d->out_states;
   p.sh_out_picks = d->out_picks;
+  p.sh_masses = d->masses;
+  p.sh_out_masses = d->out_masses;
   p.n_shards = d->n_shards;
   p.shard_index = d->shard_index;
   p.nrows = sd->rows;
@@ -3274,15 +3349,23 @@ static int launch_full(const Plan& pl, int rows, const Params& p, hipStream_t s)
 extern "C" int dsv41_sampler_full_state_run(const dsv41_sampler_full_shard_desc* d, void* stream) {
   Plan pl;
   Params p;
-  int rc = full_shard_params(d, false, &pl, &p);
+  int rc = full_shard_params(d, 0, &pl, &p);
   if (rc != DSV41_OK) return rc;
   return launch_full<DRAW_STATE>(pl, d->sampler->rows, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsv41_sampler_full_mass_run(const dsv41_sampler_full_shard_desc* d, void* stream) {
+  Plan pl;
+  Params p;
+  int rc = full_shard_params(d, 1, &pl, &p);
+  if (rc != DSV41_OK) return rc;
+  return launch_full<DRAW_SHARD_MASS>(pl, d->sampler->rows, p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int dsv41_sampler_full_draw_run(const dsv41_sampler_full_shard_desc* d, void* stream) {
   Plan pl;
   Params p;
-  int rc = full_shard_params(d, true, &pl, &p);
+  int rc = full_shard_params(d, 2, &pl, &p);
   if (rc != DSV41_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (d->sampler->exponentials) return launch_full<DRAW_SHARD_RACE>(pl, d->sampler->rows, p, s);

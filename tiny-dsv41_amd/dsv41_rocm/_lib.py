@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).with_name("libdsv41hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -245,6 +245,8 @@ class SamplerFullShardDesc(ctypes.Structure):
         ("states", ctypes.c_void_p),
         ("out_states", ctypes.c_void_p),
         ("out_picks", ctypes.c_void_p),
+        ("masses", ctypes.c_void_p),
+        ("out_masses", ctypes.c_void_p),
     ]
 
 
@@ -305,6 +307,7 @@ EXPORTS = (
     "dsv41_sampler_shard_run",
     "dsv41_sampler_merge_run",
     "dsv41_sampler_full_state_run",
+    "dsv41_sampler_full_mass_run",
     "dsv41_sampler_full_draw_run",
     "dsv41_sampler_full_finish_run",
 )
@@ -361,7 +364,7 @@ def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.dsv41_sampler_shard_run.argtypes = [ctypes.POINTER(SamplerShardDesc), ctypes.c_void_p]
     lib.dsv41_sampler_merge_run.restype = ctypes.c_int
     lib.dsv41_sampler_merge_run.argtypes = [ctypes.POINTER(SamplerMergeDesc), ctypes.c_void_p]
-    for name in ("dsv41_sampler_full_state_run", "dsv41_sampler_full_draw_run"):
+    for name in ("dsv41_sampler_full_state_run", "dsv41_sampler_full_mass_run", "dsv41_sampler_full_draw_run"):
         getattr(lib, name).restype = ctypes.c_int
         getattr(lib, name).argtypes = [ctypes.POINTER(SamplerFullShardDesc), ctypes.c_void_p]
     lib.dsv41_sampler_full_finish_run.restype = ctypes.c_int

@@ -380,9 +380,65 @@ def _gathered(parts, words: int, what: str) -> torch.Tensor:
     return t.contiguous()
 
 
+def _shard_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                frequency_penalty, vocab_offset, vocab_size, states, shard_index):
+    """Descriptor of one slice for the mass and draw steps, with the gathered states."""
+    rows, width = logits.shape
+    if not (0 <= vocab_offset and vocab_offset + width <= vocab_size):
+        raise ValueError("the slice must lie within the vocabulary")
+    st = _gathered(states, _lib.FULL_STATE_BYTES // 8, "states").to(logits.device)
+    if st.shape[1] != rows:
+        raise ValueError("states must hold one state per row of every slice")
+    if not 0 <= shard_index < st.shape[0]:
+        raise ValueError("shard_index must name one of the gathered slices")
+    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                      frequency_penalty, 0, 1.0, 0.0)
+    d = _lib.SamplerFullShardDesc()
+    d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullShardDesc)
+    d.n_shards = st.shape[0]
+    d.vocab_offset, d.vocab_size = vocab_offset, vocab_size
+    d.shard_index = shard_index
+    d.states = st.data_ptr()
+    return d, desc, st
+
+
+def full_shard_masses(
+    logits: torch.Tensor,
+    states,
+    *,
+    shard_index: int,
+    vocab_offset: int,
+    vocab_size: int,
+    temperature: float = 1.0,
+    history: Optional[torch.Tensor] = None,
+    history_lens: Optional[torch.Tensor] = None,
+    repetition_penalty: float = 1.0,
+    presence_penalty: float = 0.0,
+    frequency_penalty: float = 0.0,
+) -> torch.Tensor:
+    """Step 2 of a full-vocabulary inverse-CDF draw over slices: with every slice's state
+    gathered (``states``: a list in slice order, or int64 ``[n_shards, rows, 4]``), this slice's
+    exact fixed-point mass ``sum_i floor(2^43 exp(z_i - M))`` against the row's maximum ``M``
+    over all slices.  Returns int64 ``[rows]`` (the bits of the u64 masses); gather them from
+    every slice for :func:`full_shard_draw`.  The exponential race skips this step."""
+    logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
+    d, desc, st = _shard_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                              frequency_penalty, vocab_offset, vocab_size, states, shard_index)
+    masses = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
+    d.sampler = _lib.ctypes.pointer(desc)
+    d.out_masses = masses.data_ptr()
+    lib = _lib.load()
+    with torch.cuda.device(logits.device):
+        stream = torch.cuda.current_stream(logits.device).cuda_stream
+        rc = lib.dsv41_sampler_full_mass_run(_lib.ctypes.byref(d), stream)
+    _lib.check(rc)
+    return masses
+
+
 def full_shard_draw(
     logits: torch.Tensor,
     states,
+    masses=None,
     *,
     shard_index: int,
     vocab_offset: int,
@@ -396,25 +452,21 @@ def full_shard_draw(
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
 ) -> torch.Tensor:
-    """Step 2 of a full-vocabulary draw over slices: with every slice's state gathered
-    (``states``: a list in slice order, or int64 ``[n_shards, rows, 4]``), this slice places the
-    token when its share of the row's total holds ``u * S`` (inverse CDF against ``uniforms``,
-    the same fp32 ``[rows]`` on every slice), or reports its best ``p / E`` over its columns
-    (``exponentials``: this slice's columns of the rows' Exp(1) variates, the exponential race
-    that reproduces ``torch.multinomial``).  Returns int64 ``[rows, 2]`` (the 16-byte
+    """Step 3 of a full-vocabulary draw over slices, with every slice's state gathered
+    (``states``: a list in slice order, or int64 ``[n_shards, rows, 4]``).  Inverse CDF (against
+    ``uniforms``, the same fp32 ``[rows]`` on every slice): with every slice's exact mass
+    gathered too (``masses``: a list of the int64 ``[rows]`` of :func:`full_shard_masses`, or
+    ``[n_shards, rows]``), the slice whose masses hold the target places the token, exactly as
+    the unsharded sampler would.  Exponential race (``exponentials``: this slice's columns of
+    the rows' Exp(1) variates, which reproduce ``torch.multinomial``): each slice reports its
+    best ``p / E`` over its columns.  Returns int64 ``[rows, 2]`` (the 16-byte
     ``dsv41_full_pick``) for :func:`full_shard_finish`.  Greedy rows need no draw step."""
     logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
-    rows, width = logits.shape
-    if not (0 <= vocab_offset and vocab_offset + width <= vocab_size):
-        raise ValueError("the slice must lie within the vocabulary")
+    rows = logits.shape[0]
     device = logits.device
-    st = _gathered(states, _lib.FULL_STATE_BYTES // 8, "states").to(device)
-    if st.shape[1] != rows:
-        raise ValueError("states must hold one state per row of every slice")
-    if not 0 <= shard_index < st.shape[0]:
-        raise ValueError("shard_index must name one of the gathered slices")
-    desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
-                      frequency_penalty, 0, 1.0, 0.0)
+    d, desc, st = _shard_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
+                              frequency_penalty, vocab_offset, vocab_size, states, shard_index)
+    ms = None
     if exponentials is not None:
         exponentials = exponentials.to(device=device, dtype=torch.float32)
         if exponentials.shape != logits.shape:
@@ -430,14 +482,15 @@ def full_shard_draw(
         if uniforms.shape != (rows,):
             raise ValueError("one uniform is required per row")
         desc.uniforms = uniforms.data_ptr()
+        if masses is None:
+            raise ValueError("a sharded inverse-CDF draw needs the masses gathered from every slice")
+        ms = torch.stack(list(masses)) if isinstance(masses, (list, tuple)) else masses
+        if ms.shape != (st.shape[0], rows) or ms.dtype != torch.int64:
+            raise ValueError("masses must be the int64 [n_shards, rows] gathered from every slice")
+        ms = ms.to(device).contiguous()
+        d.masses = ms.data_ptr()
     picks = torch.empty(rows, _lib.FULL_PICK_BYTES // 8, dtype=torch.int64, device=device)
-    d = _lib.SamplerFullShardDesc()
-    d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullShardDesc)
-    d.n_shards = st.shape[0]
     d.sampler = _lib.ctypes.pointer(desc)
-    d.vocab_offset, d.vocab_size = vocab_offset, vocab_size
-    d.shard_index = shard_index
-    d.states = st.data_ptr()
     d.out_picks = picks.data_ptr()
     lib = _lib.load()
     with torch.cuda.device(device):
@@ -456,7 +509,7 @@ def full_shard_finish(
     uniforms: Optional[torch.Tensor] = None,
     check: bool = True,
 ) -> SampleResult:
-    """Step 3 of a full-vocabulary draw over slices: the token from the gathered picks
+    """Step 4 of a full-vocabulary draw over slices: the token from the gathered picks
     (``draw`` = ``"inverse_cdf"`` or ``"exponential_race"``) or, for ``"greedy"``, from the
     states alone, and its log-prob ``(z - M) - log S`` against the row's maximum and total.
     Returns what :func:`sample` returns for the unsharded logits; ``uniforms`` (inverse CDF)

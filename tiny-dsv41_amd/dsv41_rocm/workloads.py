@@ -71,11 +71,12 @@ def _gen(device, seed):
     return g
 
 
-def sampler_inputs(name: str, rows: Optional[int] = None, device="cpu"):
-    """Returns dict(logits, history, uniforms, knobs) for sampler config A, B or E."""
+def sampler_inputs(name: str, rows: Optional[int] = None, device="cpu", seed: Optional[int] = None):
+    """Returns dict(logits, history, uniforms, knobs) for sampler config A, B or E.  ``seed``
+    (default: the config's own) draws other batches of the same distribution."""
     cfg = SAMPLER_CONFIGS[name]
     rows = cfg.rows if rows is None else rows
-    g = _gen(device, SEED_BASE + cfg.index)
+    g = _gen(device, SEED_BASE + cfg.index if seed is None else seed)
     V = cfg.vocab
     if cfg.zipf:
         noise = torch.randn(rows, V, generator=g, device=device)
