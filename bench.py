@@ -2,8 +2,11 @@
 
 Default line (the driver's N=1 run): config E, the sort-heavy large-batch sampler
 (4096 rows x vocab 151936 fp32, history 4096, T 0.6, repetition 1.05, top-k 1024,
-top-p 0.98, min-p 0.05), plus a ``logprob`` object for config D (16384 tokens x hidden
-7168 -> vocab 129280 with the Token-TIS ratio) when that kernel is built.
+top-p 0.98, min-p 0.05), a ``logprob`` object for config D (16384 tokens x hidden 7168 ->
+vocab 129280 with the Token-TIS ratio, plus its backward), and an ``extra`` object with the
+other configurations, each with its own roofline and CPU baseline: sampler B (256 x 151936
+bf16, full-vocabulary draw), sampler A (8 x 129280 fp32, top-k 50 + top-p) and log-prob C
+(8192 x 2048 -> 151936), plus the B=1 decode step of ``generate_group`` at V=151936.
 
 A step is one launch over one batch with inputs already resident in HBM.  Times come
 from HIP events on the stream the kernels are launched on, over K back-to-back steps.
@@ -11,7 +14,8 @@ The roofline ``achieved`` figure is algorithmic bytes (sampler) or FLOPs (log-pr
 per launch over the measured average launch time:
   sampler bytes/row = V*sizeof(logit) + L_hist*8 + 4 (u) + 8 (id) + 4 (lp) + 4 (kept)
   log-prob FLOPs/token = 2*H*V
-``cpu_baseline`` times the C oracle (a port of the same specification) on the host.
+``cpu_baseline`` times the C oracle (a port of the same specification) or the reference
+expression on the host, on a bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -33,11 +37,13 @@ BF16_PEAK_TFLOPS = 2500.0
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by
 # the same counters on a plain 1 GiB copy (FETCH x 2.0, WRITE x 1.0); the commands and raw
-# counts are in profiles/sampler_topk_E.md, profiles/logprob_fused_D.md and
-# profiles/logprob_backward_D.md.  Workloads without an entry report null.
+# counts are in the profiles/ summaries of each kernel and workload.
 MEASURED_TRAFFIC = {
     "sampler_E": 2_629_506_528 + 1_937_544,  # topk_kernel + select_kernel
+    "sampler_B": 160_335_872 + 32_768,  # full_kernel (profiles/sampler_full_B.md)
+    "sampler_A": 5_004_270 + 393_216 + 79_872,  # sliced topk_kernel + merge_kernel
     "logprob_D": 46_112_195_686 + 1_048_576,
+    "logprob_C": 7_592_285_070 + 1_245_184,  # fused_kernel + merge_kernel
     "logprob_grad_D": 45_297_095_573 + 4_384_320_091,
 }
 
@@ -54,11 +60,12 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="E", choices=["A", "B", "E", "none"],
-                    help="sampler config; 'none' runs only the log-prob leg (for profiling)")
+                    help="headline sampler config; 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
     ap.add_argument("--logprob-steps", type=int, default=10)
     ap.add_argument("--no-backward", action="store_true", help="skip the log-prob backward timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configurations and the decode step")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="time a plain device copy of this many bytes (PMC calibration) and exit")
     return ap.parse_args()
@@ -85,7 +92,7 @@ def copy_calibration(nbytes, steps, torch):
     print(json.dumps({"copy_bytes": nbytes, "ms": ms, "GBps": 2 * nbytes / ms / 1e6}), flush=True)
 
 
-def bench_sampler(name, steps, warmup, cpu_baseline, torch):
+def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0):
     from dsv41_rocm import _lib, workloads
 
     cfg = workloads.SAMPLER_CONFIGS[name]
@@ -152,11 +159,11 @@ def bench_sampler(name, steps, warmup, cpu_baseline, torch):
                      "bytes_per_row": per_row},
     }
     if cpu_baseline:
-        line["cpu_baseline"] = cpu_sampler_baseline(inp, knobs, torch)
+        line["cpu_baseline"] = cpu_sampler_baseline(inp, knobs, torch, cpu_seconds)
     return line
 
 
-def cpu_sampler_baseline(inp, knobs, torch):
+def cpu_sampler_baseline(inp, knobs, torch, seconds=10.0):
     """C oracle (port of the same spec), one thread, on a bounded row sample of the batch;
     plus the reference's full-vocab expression (rollout.py:144-148) for context."""
     import numpy as np
@@ -164,7 +171,7 @@ def cpu_sampler_baseline(inp, knobs, torch):
     import oracle
 
     cores = len(os.sched_getaffinity(0))
-    sample_rows = min(inp["logits"].shape[0], 512)
+    sample_rows = min(inp["logits"].shape[0], 512 if seconds >= 10.0 else 64)
     x = inp["logits"][:sample_rows].float().cpu().numpy()
     h = inp["history"][:sample_rows].cpu().numpy()
     u = inp["uniforms"][:sample_rows].cpu().numpy()
@@ -173,7 +180,7 @@ def cpu_sampler_baseline(inp, knobs, torch):
     while True:
         oracle.sample(x, uniforms=u, history=h, **knobs)
         n += sample_rows
-        if time.perf_counter() - t0 > 10.0:
+        if time.perf_counter() - t0 > seconds:
             break
     dt = time.perf_counter() - t0
     out = {"value": n / dt, "unit": "rows/s", "cores": 1, "kind": "port",
@@ -188,7 +195,7 @@ def cpu_sampler_baseline(inp, knobs, torch):
         torch.set_num_threads(threads)
         t0 = time.perf_counter()
         reps = 0
-        while time.perf_counter() - t0 < 3.0:
+        while time.perf_counter() - t0 < min(3.0, seconds):
             for r in range(xt.shape[0]):
                 lp = torch.log_softmax(xt[r] / T, dim=-1)
                 p = lp.exp()
@@ -203,23 +210,104 @@ def cpu_sampler_baseline(inp, knobs, torch):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (rows and tokens are "
-              "independent, see DESIGN.md for how the path shards)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: every GPU box here has one "
+              "GPU, and rows and tokens shard with no exchange (DESIGN.md, 'More than one GPU')",
+              file=sys.stderr)
         sys.exit(2)
     import torch
 
     if args.copy_bytes:
         copy_calibration(args.copy_bytes, args.steps, torch)
         return
+    cpu = not args.no_cpu_baseline
     if args.workload == "none":
         line = {}
     else:
-        line = bench_sampler(args.workload, args.steps, args.warmup, not args.no_cpu_baseline, torch)
+        line = bench_sampler(args.workload, args.steps, args.warmup, cpu, torch)
         print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
-        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 3, not args.no_cpu_baseline, torch,
+        line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 3, cpu, torch,
                                         backward=not args.no_backward)
+    if not args.no_extra:
+        extra = {}
+        for name in ("B", "A"):
+            if name != args.workload:
+                extra[f"sampler_{name}"] = bench_sampler(name, 200, 20, cpu, torch, cpu_seconds=4.0)
+                print(json.dumps({name: extra[f"sampler_{name}"]["ms_per_step"]}), file=sys.stderr, flush=True)
+        if args.logprob != "C":
+            extra["logprob_C"] = bench_logprob("C", 20, 3, cpu, torch, backward=False)
+        extra["decode_B1"] = bench_decode(torch)
+        line["extra"] = extra
     print(json.dumps(line), flush=True)
+
+
+def bench_decode(torch, tokens=200, warmup=20):
+    """The per-token sampling step of generate_group at batch 1 (rollout.py:144-148) on one
+    [1, 151936] fp32 logits row resident on the GPU, wall clock per token:
+    * reference: log_softmax(logits / T) on the GPU, the finite check (a sync), exp, the
+      4V-byte copy to the host, torch.multinomial on one CPU thread (rl/config.py:45,
+      pytorch_rl.py:39), and the behaviour log-prob read back (another sync);
+    * race: sample_next(draw="exponential_race"), which draws the reference's token: V Exp(1)
+      variates from the CPU generator (the reference's own RNG work), their 4V-byte copy to
+      the GPU, the kernel, two scalars back;
+    * inverse_cdf: sample_next(draw="inverse_cdf"): one uniform, the kernel, two scalars back."""
+    from dsv41_rocm import sample_next, workloads
+
+    dev = torch.device("cuda:0")
+    row = workloads.sampler_inputs("B", rows=1, device=dev)["logits"].float()
+    T = 1.0
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)
+
+    def reference(g):
+        log_probs = torch.log_softmax(row[0].float() / T, dim=-1)
+        if not torch.isfinite(log_probs).all().item():
+            raise ValueError("generation log probabilities contain non-finite values")
+        probabilities = log_probs.exp().cpu()
+        token = int(torch.multinomial(probabilities, 1, generator=g).item())
+        return token, float(log_probs[token].item())
+
+    def timed(fn):
+        g = torch.Generator().manual_seed(1234)
+        for _ in range(warmup):
+            fn(g)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = [fn(g) for _ in range(tokens)]
+        dt = (time.perf_counter() - t0) / tokens
+        return dt * 1e6, out
+
+    ref_us, ref_out = timed(reference)
+    race_us, race_out = timed(lambda g: sample_next(row, T, generator=g, draw="exponential_race"))
+    cdf_us, _ = timed(lambda g: sample_next(row, T, generator=g, draw="inverse_cdf"))
+    # the race's host share: the V exponentials and their copy to the GPU
+    V = row.shape[1]
+    g = torch.Generator().manual_seed(1)
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        e = torch.empty(1, V, dtype=torch.float32).exponential_(1, generator=g)
+    fill_us = (time.perf_counter() - t0) / tokens * 1e6
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        e.to(dev)
+    torch.cuda.synchronize()
+    h2d_us = (time.perf_counter() - t0) / tokens * 1e6
+    torch.set_num_threads(threads)
+    same = sum(int(a[0] == b[0]) for a, b in zip(ref_out, race_out))
+    return {
+        "metric": "sampling step latency at batch 1 (rollout.py:144-148)",
+        "unit": "us/token",
+        "vocab": V,
+        "tokens": tokens,
+        "reference_step_us": ref_us,
+        "race_us": race_us,
+        "inverse_cdf_us": cdf_us,
+        "race_host_exponentials_us": fill_us,
+        "race_h2d_copy_us": h2d_us,
+        "race_ids_equal_reference": f"{same}/{tokens}",
+        "note": "wall clock per token, logits resident on the GPU, host on 1 thread as the reference sets it",
+    }
 
 
 def bench_logprob(name, steps, warmup, cpu_baseline, torch, backward=False):
