@@ -75,9 +75,10 @@ extern "C" {
  *   top-p  (top_p < 1): keep the shortest prefix of that order whose 2^-43 fixed-point
  *                       mass reaches ceil(top_p * total);
  *   draw: inverse CDF in vocabulary order over the kept set against uniforms[r], on the
- *         2^-43 fixed-point masses floor(2^43 exp(z_i - z_max)): the first token whose
- *         cumulative mass exceeds (total * floor(u * 2^32)) >> 32, exact in integers
- *         (greedy != 0: first index of max z instead);
+ *         2^-43 fixed-point masses floor(2^43 exp(z_i - z_max)) (exp evaluated by a fixed
+ *         sequence of fp32 operations, identical on every device and in the oracle): the
+ *         first token whose cumulative mass exceeds (total * floor(u * 2^32)) >> 32, exact
+ *         in integers (greedy != 0: first index of max z instead);
  *   out_logprob = z_tok - log(sum_kept exp(z)), out_kept = kept-set size.
  * history[r * history_row_stride + j], j < (history_lens ? history_lens[r] : hist_len);
  * negative ids are padding and ignored.

@@ -19,8 +19,9 @@
  * Exactness: every decision that selects tokens is made in IEEE fp32 compares,
  * exact fp64 differences of fp32 values, and 64-bit fixed-point masses
  * (2^-43 resolution) whose sums are associative, so any reduction order gives the
- * same kept set and the same drawn id.  The only transcendental on that path is
- * dsv41_exp_det() below, a fixed sequence of fp64 mul/fma/rint operations.
+ * same kept set and the same drawn id.  The only transcendental on that path is the
+ * exponential inside dsv41_mass() below, a fixed sequence of fp32 operations; the
+ * log-prob uses dsv41_exp_det(), a fixed sequence of fp64 operations.
  *
  * Every function here is pinned by tests/test_oracle_sampler.py against closed
  * forms (log_softmax in fp64, libm exp), brute force on tiny vocabularies, and
@@ -71,10 +72,27 @@ double dsv41_exp_det(double d) {
   return p * scale;
 }
 
-/* Fixed-point mass of a token: floor(2^43 * exp_det(z - zmax)). */
+/* Fixed-point mass of a token: floor(2^43 * e) with e = exp(z - zmax) evaluated by a fixed
+ * sequence of fp32 operations: d = z - zmax (fp32), 0 for d < -40 and NaN; Cody-Waite
+ * reduction by a two-part ln 2, a degree-7 Taylor polynomial in Horner form with fma, and an
+ * exact scale by 2^(n + 43).  Every step is an IEEE fp32 operation (fmaf, rintf, ldexpf,
+ * floorf are exact or correctly rounded), so the device computes the same integer. */
 uint64_t dsv41_mass(float z, float zmax) {
-  double e = dsv41_exp_det((double)z - (double)zmax);
-  return (uint64_t)(e * 8796093022208.0); /* 2^43 */
+  float d = z - zmax;
+  if (!(d >= -40.0f)) return 0;
+  if (d > 0.0f) d = 0.0f;
+  float n = rintf(d * 0x1.715476p+0f);   /* log2(e) */
+  float r = fmaf(-n, 0x1.62e4p-1f, d);    /* ln 2, high part (exact products) */
+  r = fmaf(-n, 0x1.7f7d1cp-20f, r);       /* ln 2, low part */
+  float p = 0x1.a01a02p-13f;              /* 1/7! */
+  p = fmaf(p, r, 0x1.6c16c2p-10f);        /* 1/6! */
+  p = fmaf(p, r, 0x1.111112p-7f);         /* 1/5! */
+  p = fmaf(p, r, 0x1.555556p-5f);         /* 1/4! */
+  p = fmaf(p, r, 0x1.555556p-3f);         /* 1/3! */
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return (uint64_t)floorf(ldexpf(p, (int)n + 43));
 }
 
 /* ceil(p * s) exactly, p a positive fp32 <= 1. */

@@ -34,13 +34,31 @@ def test_exp_det_matches_libm_within_two_ulp():
 
 
 def test_mass_is_floor_of_2_43_times_exp():
+    # the mass is floor(2^43 exp(d)) of the fp32 difference d = z - zmax, evaluated in fp32:
+    # against libm's exp of the same d it is within 2^-22 relative plus the floor's unit
     rng = random.Random(2)
-    for _ in range(5000):
+    worst = 0.0
+    for _ in range(20000):
         z, zmax = np.float32(rng.uniform(-30, 10)), np.float32(rng.uniform(10, 20))
+        d = float(np.float32(z - zmax))
         q = oracle.mass(float(z), float(zmax))
-        e = math.exp(float(z) - float(zmax))
-        assert abs(q - math.floor(e * TWO43)) <= 1
-    assert oracle.mass(3.0, 3.0) == TWO43
+        e = math.ldexp(math.exp(d), 43)
+        assert abs(q - math.floor(e)) <= e * 2.0 ** -22 + 1, (z, zmax, q, e)
+        if e > 1e7:
+            worst = max(worst, abs(q - e) / e)
+    assert worst <= 2.0 ** -22
+    # every integer is exact where no rounding is involved
+    assert oracle.mass(3.0, 3.0) == TWO43 and oracle.mass(-7.5, -7.5) == TWO43
+    for n in range(0, 40):  # the reduction's edge cases: d = fl(-n ln 2), where r is near 0
+        d = float(np.float32(-n * math.log(2)))
+        e = math.ldexp(math.exp(d), 43)
+        assert abs(oracle.mass(d, 0.0) - e) <= e * 2.0 ** -22 + 1
+    # below -40 and for NaN the mass is 0; the masses are non-decreasing in z on a fine grid
+    assert oracle.mass(-40.001, 0.0) == 0 and oracle.mass(float("nan"), 0.0) == 0
+    assert oracle.mass(float("-inf"), 0.0) == 0
+    grid = np.float32(-np.linspace(0, 39.9, 40001))[::-1]
+    qs = [oracle.mass(float(v), 0.0) for v in grid]
+    assert all(a <= b for a, b in zip(qs, qs[1:]))
 
 
 def test_top_p_threshold_is_exact_ceiling():
@@ -122,7 +140,7 @@ def test_draw_is_inverse_cdf_in_vocabulary_order():
         u = np.array([rng.random()], np.float32)
         ids, _, _, _ = oracle.sample(x, uniforms=u, temperature=1.0)
         zmax = float(x[0].max())
-        q = [math.floor(math.exp(float(v) - zmax) * TWO43) for v in x[0]]
+        q = [oracle.mass(float(v), zmax) for v in x[0]]  # the mass itself is pinned above
         t = (sum(q) * math.floor(Fraction(float(u[0])) * (1 << 32))) >> 32
         cum, want = 0, None
         for i, qi in enumerate(q):
@@ -144,7 +162,7 @@ def _brute_kept(z, k, p, min_p):
     if 0 < k < len(order):
         order = order[:k]
     if p < 1:
-        q = [math.floor(math.exp(float(z[i]) - zmax) * TWO43) for i in order]
+        q = [oracle.mass(float(z[i]), float(zmax)) for i in order]  # pinned by the mass test
         thr = math.ceil(Fraction(float(np.float32(p))) * sum(q))
         cum = 0
         for n, qi in enumerate(q):

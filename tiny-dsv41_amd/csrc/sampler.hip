@@ -232,42 +232,32 @@ __device__ __forceinline__ double exp_det(double d) {
   return p * __longlong_as_double(e << 52);
 }
 
-// floor(2^43 exp_det(z - M)) as an (exact, integer-valued) double.  The same operations as
-// exp_det, arranged for the vector unit: the range checks become a clamp and one select,
-// and the scale by 2^n and by 2^43 is one ldexp with a 32-bit exponent.  Every step is
-// exact except the ones exp_det rounds identically, so the floor is the spec's bit for bit.
-__device__ __forceinline__ double mass_f(float z, double M) {
-  double d = (double)z - M;
-  const bool ok = d >= -40.0;  // false for NaN
-  d = fmin(fmax(d, -40.0), 0.0);
-  const double log2e = 1.4426950408889634074;
-  const double ln2_hi = 6.93147180369123816490e-01;
-  const double ln2_lo = 1.90821492927058770002e-10;
-  const double n = __builtin_rint(d * log2e);
-  double r = __builtin_fma(-n, ln2_hi, d);
-  r = __builtin_fma(-n, ln2_lo, r);
-  double p = 1.0 / 6227020800.0;
-  p = __builtin_fma(p, r, 1.0 / 479001600.0);
-  p = __builtin_fma(p, r, 1.0 / 39916800.0);
-  p = __builtin_fma(p, r, 1.0 / 3628800.0);
-  p = __builtin_fma(p, r, 1.0 / 362880.0);
-  p = __builtin_fma(p, r, 1.0 / 40320.0);
-  p = __builtin_fma(p, r, 1.0 / 5040.0);
-  p = __builtin_fma(p, r, 1.0 / 720.0);
-  p = __builtin_fma(p, r, 1.0 / 120.0);
-  p = __builtin_fma(p, r, 1.0 / 24.0);
-  p = __builtin_fma(p, r, 1.0 / 6.0);
-  p = __builtin_fma(p, r, 0.5);
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
-  const double f = __builtin_floor(__builtin_ldexp(p, (int)n + 43));
-  return ok ? f : 0.0;
+// Fixed-point mass of a token, floor(2^43 * exp(z - zmax)), as an exact integer-valued
+// float: the same fp32 operations as the oracle's specification (d = z - zmax, 0 below -40
+// and for NaN; Cody-Waite reduction by a two-part ln 2; degree-7 Taylor polynomial in
+// Horner form with fma; exact scale by 2^(n + 43); floor).  The range checks are a clamp
+// and one select here; every step is exact or correctly rounded, so the integer is the
+// oracle's bit for bit.  The result has at most 24 significant bits and is at most 2^43.
+__device__ __forceinline__ float mass_ff(float z, float zmax) {
+  float d = z - zmax;
+  const bool ok = d >= -40.0f;  // false for NaN
+  d = fminf(fmaxf(d, -40.0f), 0.0f);
+  const float n = __builtin_rintf(d * 0x1.715476p+0f);
+  float r = __builtin_fmaf(-n, 0x1.62e4p-1f, d);
+  r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const float f = __builtin_floorf(__builtin_ldexpf(p, (int)n + 43));
+  return ok ? f : 0.0f;
 }
 
-// Fixed-point mass of a token: floor(2^43 * exp_det(z - zmax)).
-__device__ __forceinline__ uint64_t mass_of(float z, float zmax) {
-  return (uint64_t)mass_f(z, (double)zmax);
-}
+__device__ __forceinline__ uint64_t mass_of(float z, float zmax) { return (uint64_t)mass_ff(z, zmax); }
 
 __device__ __forceinline__ uint64_t top_p_threshold(float p, uint64_t s) {
   uint32_t bits = __float_as_uint(p);
@@ -1136,7 +1126,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     return;
   }
 
-  // Inverse-CDF draws use 2^-43 fixed-point masses q_i = floor(2^43 exp_det(z_i - Mref))
+  // Inverse-CDF draws use 2^-43 fixed-point masses q_i = floor(2^43 exp(z_i - Mref))
   // against the row's maximum Mref (a slice: the maximum over all slices), as the oracle and
   // the truncating kernels do.  Integer sums are associative, so the drawn id does not depend
   // on the order of any reduction.  A second pass over the row sums each chunk's masses into
@@ -1176,7 +1166,6 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   }
   if (exact) {
     const int nt = (p.V + TILE - 1) / TILE;
-    const double Md = (double)Mref;
     Raw<TIn, G> R0, R1;
     load_group<TIn, G, VEC>(R0, rs, tid * G);
     for (int t = 0; t < nt; ++t) {
@@ -1189,7 +1178,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       // the G masses are integers of at most 2^43: their sum is exact in fp64
       double qd = 0.0;
 #pragma unroll
-      for (int j = 0; j < G; ++j) qd += mass_f(z[j], Md);
+      for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], Mref);
       uint64_t q = (uint64_t)qd;
       q = wave_sum_u64(q);
       const int c = t * NW + wid;
@@ -2324,7 +2313,7 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
             for (int j = 0; j < G; ++j) {
               const double d = (double)z[j] - dmax;
               if (d >= -30.0) {
-                const uint64_t ms = (uint64_t)(exp_det(d) * 8796093022208.0);
+                const uint64_t ms = mass_of(z[j], zmax);
                 tot += ms;
                 if (ms) atomicAdd((unsigned long long*)&bins[topp_bin(z[j], zmax)], (unsigned long long)ms);
                 if (d >= (double)db) offer(z[j], base + j);
@@ -2400,7 +2389,7 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
       const int b = topp_bin(z, zmax);
       if (b < bstar) {
         const double e = exp_det((double)z - dmax);
-        atomicAdd((unsigned long long*)&chunks[ckey_idx(key) / CH], (unsigned long long)(e * 8796093022208.0));
+        atomicAdd((unsigned long long*)&chunks[ckey_idx(key) / CH], (unsigned long long)mass_of(z, zmax));
         es += e;
         ++nk;
       } else if (b == bstar) {
@@ -2428,7 +2417,7 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
                   const int b = topp_bin(z[j], zmax);
                   if (b < bstar) {
                     const double e = exp_det(d);
-                    cs += (uint64_t)(e * 8796093022208.0);
+                    cs += mass_of(z[j], zmax);
                     es += e;
                     ++nk;
                   } else if (b == bstar) {
@@ -2453,7 +2442,7 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
               const int b = topp_bin(z, zmax);
               if (b < bstar) {
                 const double e = exp_det(d);
-                atomicAdd((unsigned long long*)&chunks[tok / CH], (unsigned long long)(e * 8796093022208.0));
+                atomicAdd((unsigned long long*)&chunks[tok / CH], (unsigned long long)mass_of(z, zmax));
                 es += e;
                 ++nk;
               } else if (b == bstar) {
@@ -2496,7 +2485,7 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
   for (int j = tid; j <= jstar; j += NT) {
     const uint64_t key = blist[j];
     const double e = exp_det((double)ckey_z(key) - dmax);
-    atomicAdd((unsigned long long*)&chunks[ckey_idx(key) / CH], (unsigned long long)(e * 8796093022208.0));
+    atomicAdd((unsigned long long*)&chunks[ckey_idx(key) / CH], (unsigned long long)mass_of(ckey_z(key), zmax));
     es += e;
     ++nk;
   }
@@ -2545,7 +2534,7 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
         zz[j] = z;
         ms[j] = 0;
         const double d = (double)z - dmax;
-        if (d >= -30.0 && ckey(z, (uint32_t)idx) >= Bkey) ms[j] = (uint64_t)(exp_det(d) * 8796093022208.0);
+        if (d >= -30.0 && ckey(z, (uint32_t)idx) >= Bkey) ms[j] = mass_of(z, zmax);
         ls += ms[j];
       }
       const uint64_t incl = wave_incl_scan_u64(ls, lane) + before;
