@@ -83,6 +83,8 @@ def _sampler_desc(**kw):
     (dict(logits_row_stride=50), _lib.E_INVALID, "stride"),
     (dict(uniforms=None), _lib.E_INVALID, "uniform"),
     (dict(vocab=(1 << 21) + 1, logits_row_stride=(1 << 21) + 1), _lib.E_UNSUPPORTED, "2^21"),
+    # 2^21 masses of 2^43 (a flat row) would sum to exactly 2^64
+    (dict(vocab=1 << 21, logits_row_stride=1 << 21), _lib.E_UNSUPPORTED, "2^21"),
     (dict(struct_size=8), _lib.E_ABI, "size mismatch"),
     (dict(exponentials=0x6000, exponentials_row_stride=100, top_k=5), _lib.E_UNSUPPORTED, "exponential race"),
     (dict(exponentials=0x6000, exponentials_row_stride=99), _lib.E_INVALID, "exponentials row stride"),

@@ -55,7 +55,7 @@ constexpr int PF = 4;                          // tiles per pipelined batch
 constexpr int TOPK_G = 4;                      // elements per thread per TOPK tile
 constexpr int TOPK_TILE = TOPK_NT * TOPK_G;    // 2048
 constexpr int KCAP = TOPK_TILE;                // largest top_k on the one-pass path
-constexpr int MAX_VOCAB = 1 << 21;             // 2^21 * 2^43 < 2^64: mass sums cannot wrap
+constexpr int MAX_VOCAB = (1 << 21) - 1;       // (2^21 - 1) masses of at most 2^43 sum below 2^64
 constexpr int MAX_UNIQUE = 65535;              // history slots and counts are 16-bit
 constexpr int DEFER_KEYS = 4 * 64;             // candidates a one-wave final selection holds
 constexpr int DEFER_MIN_ROWS = 256;            // batches above one row per CU defer it
@@ -2814,7 +2814,7 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
     return fail(DSV41_E_ABI, "dsv41_sampler_desc size mismatch (rebuild the binding)");
   if (d->rows <= 0 || d->vocab <= 0)
     return fail(DSV41_E_INVALID, "logits must have shape [rows, vocabulary_size] with both nonzero");
-  if (d->vocab > MAX_VOCAB) return fail(DSV41_E_UNSUPPORTED, "vocabulary_size above 2^21 is not supported");
+  if (d->vocab > MAX_VOCAB) return fail(DSV41_E_UNSUPPORTED, "vocabulary_size of 2^21 or more is not supported");
   if (d->logits_dtype != DSV41_DTYPE_F32 && d->logits_dtype != DSV41_DTYPE_BF16)
     return fail(DSV41_E_INVALID, "logits dtype must be float32 or bfloat16");
   if (!d->logits || d->logits_row_stride < d->vocab)
@@ -3223,7 +3223,7 @@ extern "C" int dsv41_sampler_shard_run(const dsv41_sampler_shard_desc* d, void* 
   if (pl.mode != MODE_TOPK)
     return fail(DSV41_E_UNSUPPORTED, "vocabulary-sharded sampling needs 1 <= top_k <= 2048");
   if (d->vocab_offset < 0 || d->vocab_size < d->vocab_offset + sd->vocab || d->vocab_size > MAX_VOCAB)
-    return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of at most 2^21 ids");
+    return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of fewer than 2^21 ids");
   if (d->max_candidates < sd->top_k) return fail(DSV41_E_INVALID, "sampler shard: max_candidates must be >= top_k");
   if (!d->out_keys || !d->out_counts || !d->out_status)
     return fail(DSV41_E_INVALID, "sampler shard: out_keys, out_counts and out_status are required");
@@ -3292,7 +3292,7 @@ static int full_shard_params(const dsv41_sampler_full_shard_desc* d, int step, P
     return fail(DSV41_E_UNSUPPORTED, "vocabulary-sharded full-vocabulary draws take no top-k, top-p or min-p");
   if (sd->replay_ids) return fail(DSV41_E_UNSUPPORTED, "sampler full shard: replay_ids are not sharded");
   if (d->vocab_offset < 0 || d->vocab_size < d->vocab_offset + sd->vocab || d->vocab_size > MAX_VOCAB)
-    return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of at most 2^21 ids");
+    return fail(DSV41_E_INVALID, "sampler shard: the slice must lie within a vocabulary of fewer than 2^21 ids");
   if (step > 0) {
     if (sd->greedy) return fail(DSV41_E_INVALID, "sampler full shard: greedy rows need no draw step (finish from the states)");
     if (d->n_shards <= 0 || d->shard_index < 0 || d->shard_index >= d->n_shards)
