@@ -174,6 +174,26 @@ def test_deferred_batches_on_both_workgroup_sizes(V, dtype, pen):
     assert_exact(gpu, ora)
 
 
+def test_sliced_merge_compacts_under_min_p():
+    """Rows of a sliced batch whose slices' lists add up to more than 256 keys go through the
+    merge's compaction (the top_k of the union within the min-p bound of its largest key), in
+    both of its branches: a peaked row where fewer than top_k keys pass min-p, and flat rows
+    where every key does, so top_k cuts the union."""
+    g = torch.Generator().manual_seed(81)
+    rows, V = 3, 151936  # 25 slices of 6144 ids per row: 25 x 64 keys per row in the union
+    x = 3.0 * torch.randn(rows, V, generator=g)
+    x[1] = 0.01 * torch.randn(V, generator=g)            # flat: all of V within the min-p bound
+    x[2] = 0.01 * torch.randn(V, generator=g)
+    x[2, 77777] = 2.0                                     # flat but one leader: bound below all
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, 200), generator=g)
+    knobs = dict(temperature=1.0, top_k=64, min_p=0.05, repetition_penalty=1.1)
+    gpu, ora = run_both(x, u, hist, **knobs)
+    assert_exact(gpu, ora)
+    kept = gpu[2]
+    assert kept[0] < 64 and kept[1] == 64 and kept[2] == 64, kept
+
+
 @pytest.mark.parametrize("rows,V,dtype,knobs", [
     (1, 151936, torch.float32, dict(top_k=50, top_p=0.95, repetition_penalty=1.1)),        # 25 slices
     (3, 129281, torch.float32, dict(top_k=256, presence_penalty=0.4, frequency_penalty=0.1)),  # odd V: scalar loads
