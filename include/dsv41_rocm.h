@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DSV41_ABI_VERSION 5
+#define DSV41_ABI_VERSION 6
 
 /* Element types of logits / activations. */
 #define DSV41_DTYPE_F32 0
@@ -66,9 +66,9 @@ extern "C" {
 
 /*
  * Row sampler.  For each row r of logits[rows, vocab]:
- *   x = float(logit); for ids with count c > 0 in the row's history:
+ *   x = float(logit); for ids in the row's history (c = count, see history_prompt_lens):
  *     x = x > 0 ? x / repetition_penalty : x * repetition_penalty;
- *     x = x - frequency_penalty * c;  x = x - presence_penalty;
+ *     x = x - frequency_penalty * c;  if (c > 0) x = x - presence_penalty;
  *   z = x / temperature;
  *   min-p  (min_p > 0): keep z_i - z_max >= log(min_p) (fp64);
  *   top-k  (top_k > 0): keep the first top_k of the survivors in (z desc, index asc);
@@ -81,7 +81,12 @@ extern "C" {
  *         in integers (greedy != 0: first index of max z instead);
  *   out_logprob = z_tok - log(sum_kept exp(z)), out_kept = kept-set size.
  * history[r * history_row_stride + j], j < (history_lens ? history_lens[r] : hist_len);
- * negative ids are padding and ignored.
+ * negative ids are padding and ignored.  With history_prompt_lens, the first
+ * history_prompt_lens[r] entries of row r are the prompt's ids and the rest the generated
+ * ones, and the penalties follow vLLM's rule: the repetition penalty applies to ids of the
+ * prompt or the output, the frequency and presence penalties count the output only (c is the
+ * id's count among the generated entries; presence applies when c > 0).  Without it every
+ * entry counts as generated.
  */
 typedef struct dsv41_sampler_desc {
   uint32_t struct_size; /* = sizeof(dsv41_sampler_desc) */
@@ -118,6 +123,7 @@ typedef struct dsv41_sampler_desc {
    * knobs (behaviour log-probs replayed exactly, rl/qwen_policy.py:156-190); out_ids echoes
    * the id.  uniforms may be NULL. */
   const int64_t* replay_ids;       /* [rows] or NULL */
+  const int32_t* history_prompt_lens; /* [rows] or NULL: leading history entries of the prompt */
 } dsv41_sampler_desc;
 
 /*

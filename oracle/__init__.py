@@ -86,6 +86,22 @@ def penalize(x: float, count: int, rp: float, pres: float, freq: float) -> float
     return lib().dsv41_penalize(x, count, rp, pres, freq)
 
 
+def process_row(logits, *, temperature=1.0, history=None, history_prompt_len=0, repetition_penalty=1.0,
+                presence_penalty=0.0, frequency_penalty=0.0):
+    """Processed logits z of one row (penalties, then / T) and the status bits."""
+    x = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+    V = x.shape[0]
+    h = np.ascontiguousarray(np.asarray([] if history is None else history, dtype=np.int64))
+    counts = np.empty(V, np.uint32)
+    z = np.empty(V, np.float32)
+    c = lib()
+    st = c.dsv41_oracle_process_row(_ptr(x), ctypes.c_int(V), _ptr(h) if h.size else None, ctypes.c_int(h.size),
+                                    ctypes.c_int(history_prompt_len), ctypes.c_float(temperature),
+                                    ctypes.c_float(repetition_penalty), ctypes.c_float(presence_penalty),
+                                    ctypes.c_float(frequency_penalty), _ptr(counts), _ptr(z))
+    return z, int(st)
+
+
 def check_division(temperature: float, lo: int, hi: int) -> tuple[int, int]:
     first = ctypes.c_uint32(0)
     n = lib().dsv41_check_division(temperature, lo, hi, ctypes.byref(first))
@@ -98,8 +114,10 @@ def _ptr(a):
 
 def sample(logits, *, temperature=1.0, uniforms=None, history=None, history_lens=None,
            repetition_penalty=1.0, presence_penalty=0.0, frequency_penalty=0.0, top_k=0,
-           top_p=1.0, min_p=0.0, greedy=False):
+           top_p=1.0, min_p=0.0, greedy=False, history_prompt_lens=None):
     """Oracle sampler over fp32 logits [rows, V] (bf16 callers widen exactly first).
+    ``history_prompt_lens[r]`` leading history entries of row r are prompt ids (repetition
+    penalty only; frequency and presence count the rest).
 
     Returns numpy (ids int64, logprobs fp32, kept int32, status int32).
     """
@@ -108,6 +126,7 @@ def sample(logits, *, temperature=1.0, uniforms=None, history=None, history_lens
     u = None if uniforms is None else np.ascontiguousarray(np.asarray(uniforms, dtype=np.float32))
     h = None if history is None else np.ascontiguousarray(np.asarray(history, dtype=np.int64))
     hl = None if history_lens is None else np.ascontiguousarray(np.asarray(history_lens, dtype=np.int32))
+    pl = None if history_prompt_lens is None else np.ascontiguousarray(np.asarray(history_prompt_lens, dtype=np.int32))
     ids = np.empty(rows, np.int64)
     lps = np.empty(rows, np.float32)
     kept = np.empty(rows, np.int32)
@@ -116,7 +135,7 @@ def sample(logits, *, temperature=1.0, uniforms=None, history=None, history_lens
     rc = c.dsv41_oracle_sample(
         _ptr(x), ctypes.c_int(rows), ctypes.c_int(vocab), _ptr(h),
         ctypes.c_int64(0 if h is None else h.shape[1]), ctypes.c_int(0 if h is None else h.shape[1]),
-        _ptr(hl), _ptr(u), ctypes.c_float(temperature), ctypes.c_float(repetition_penalty),
+        _ptr(hl), _ptr(pl), _ptr(u), ctypes.c_float(temperature), ctypes.c_float(repetition_penalty),
         ctypes.c_float(presence_penalty), ctypes.c_float(frequency_penalty), ctypes.c_int(top_k),
         ctypes.c_float(top_p), ctypes.c_float(min_p), ctypes.c_int(1 if greedy else 0), _ptr(ids),
         _ptr(lps), _ptr(kept), _ptr(status))

@@ -122,13 +122,14 @@ uint64_t dsv41_draw_target(float u, uint64_t s) {
   return (uint64_t)(((u128)s * uu) >> 32);
 }
 
-/* Penalties on one logit whose history count is c > 0 (vLLM v1 apply_penalties:
- * repetition first, then frequency * count, then presence). */
+/* Penalties on one logit of an id in the history (vLLM v1 apply_penalties: repetition for
+ * ids of the prompt or the output, then frequency * c and presence (c > 0), where c counts
+ * the id among the generated entries only). */
 float dsv41_penalize(float x, uint32_t c, float rp, float pres, float freq) {
   x = x > 0.0f ? x / rp : x * rp;
   float f = freq * (float)c;
   x = x - f;
-  x = x - pres;
+  if (c > 0) x = x - pres;
   return x;
 }
 
@@ -154,10 +155,12 @@ static int cmp_asc_u32(const void* a, const void* b) {
 }
 
 /*
- * Processed logits of one row: z[v] for v < V.  counts[] is scratch of V uint32.
+ * Processed logits of one row: z[v] for v < V.  The first plen history entries are the
+ * prompt's (membership only), the rest the generated ids (counted).  counts[] is scratch of
+ * V uint32: bit 31 marks membership, the low bits hold the generated count.
  * Returns status bits (NONFINITE / BAD_HISTORY).
  */
-int dsv41_oracle_process_row(const float* x, int V, const int64_t* hist, int hlen, float T,
+int dsv41_oracle_process_row(const float* x, int V, const int64_t* hist, int hlen, int plen, float T,
                              float rp, float pres, float freq, uint32_t* counts, float* z) {
   int status = 0;
   memset(counts, 0, sizeof(uint32_t) * (size_t)V);
@@ -171,11 +174,12 @@ int dsv41_oracle_process_row(const float* x, int V, const int64_t* hist, int hle
       status |= ST_BAD_HISTORY;
       continue;
     }
-    counts[id] += 1;
+    counts[id] |= 0x80000000u;
+    if (j >= plen) counts[id] += 1;
   }
   for (int v = 0; v < V; ++v) {
     float xv = x[v];
-    if (counts[v]) xv = dsv41_penalize(xv, counts[v], rp, pres, freq);
+    if (counts[v]) xv = dsv41_penalize(xv, counts[v] & 0x7FFFFFFFu, rp, pres, freq);
     float zv = xv / T;
     if (!isfinite(zv)) status |= ST_NONFINITE;
     z[v] = zv;
@@ -275,7 +279,8 @@ int dsv41_oracle_select_row(const float* z, int V, float u, int top_k, float top
  * Non-finite rows get id -1, NaN log-prob and kept 0.
  */
 int dsv41_oracle_sample(const float* logits, int rows, int V, const int64_t* hist,
-                        int64_t hstride, int hlen, const int32_t* hlens, const float* uniforms,
+                        int64_t hstride, int hlen, const int32_t* hlens, const int32_t* plens,
+                        const float* uniforms,
                         float T, float rp, float pres, float freq, int top_k, float top_p,
                         float min_p, int greedy, int64_t* out_ids, float* out_lp,
                         int32_t* out_kept, int32_t* out_status) {
@@ -293,7 +298,7 @@ int dsv41_oracle_sample(const float* logits, int rows, int V, const int64_t* his
   for (int r = 0; r < rows; ++r) {
     int hl = hist ? (hlens ? hlens[r] : hlen) : 0;
     int st = dsv41_oracle_process_row(logits + (size_t)r * V, V, hist ? hist + r * hstride : NULL,
-                                      hl, T, rp, pres, freq, counts, z);
+                                      hl, plens ? plens[r] : 0, T, rp, pres, freq, counts, z);
     if (st & ST_NONFINITE) {
       out_ids[r] = -1;
       out_lp[r] = NAN;

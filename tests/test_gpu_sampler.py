@@ -174,6 +174,40 @@ def test_deferred_batches_on_both_workgroup_sizes(V, dtype, pen):
     assert_exact(gpu, ora)
 
 
+@pytest.mark.parametrize("rows,V,knobs", [
+    (24, 20011, dict()),                                           # full vocabulary, inverse CDF
+    (24, 20011, dict(greedy=True)),
+    (300, 20011, dict(top_k=100, top_p=0.95, min_p=0.02)),        # deferred top-k, full tables
+    (300, 20011, dict(top_k=100, top_p=0.95, min_p=0.02, frequency_penalty=0.0)),
+    (3, 151936, dict(top_k=64, top_p=0.9)),                        # sliced small batch
+    (24, 20011, dict(top_p=0.9)),                                  # top-p alone
+    (24, 20011, dict(top_k=3000, top_p=0.97)),                     # radix path
+])
+def test_prompt_history_split(rows, V, knobs):
+    """History = prompt ids + generated ids with per-row prompt lengths: repetition for both,
+    frequency and presence for the generated ids only, on every kernel, against the oracle."""
+    g = torch.Generator().manual_seed(rows + V)
+    x = 2.0 * torch.randn(rows, V, generator=g)
+    L = 400
+    hist = torch.randint(0, V, (rows, L), generator=g)
+    hist[:, 300:] = hist[:, :100]  # generated ids that repeat prompt ids
+    plens = torch.randint(0, L + 1, (rows,), generator=g).to(torch.int32)
+    plens[0], plens[-1] = 0, L
+    u = torch.rand(rows, generator=g)
+    pen = dict(repetition_penalty=1.3, presence_penalty=0.4, frequency_penalty=0.15)
+    pen.update({k: v for k, v in knobs.items() if k.endswith("penalty")})
+    rest = {k: v for k, v in knobs.items() if not k.endswith("penalty")}
+    greedy = rest.get("greedy", False)
+    gpu, ora = run_both(x, None if greedy else u, hist, history_prompt_lens=plens, temperature=0.8, **pen, **rest)
+    assert_exact(gpu, ora)
+    # prompt lengths of 0 are the unsplit history
+    g0, o0 = run_both(x, None if greedy else u, hist, history_prompt_lens=torch.zeros(rows, dtype=torch.int32),
+                      temperature=0.8, **pen, **rest)
+    g1, _ = run_both(x, None if greedy else u, hist, temperature=0.8, **pen, **rest)
+    for a, b in zip(g0, g1):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_sliced_merge_compacts_under_min_p():
     """Rows of a sliced batch whose slices' lists add up to more than 256 keys go through the
     merge's compaction (the top_k of the union within the min-p bound of its largest key), in

@@ -212,3 +212,30 @@ def test_full_vocabulary_slices_fp32_unaligned_and_statuses(draw):
         assert st[7] & 4
     assert_full_close(res, whole, exact_ids=draw != "exponential_race")
 
+
+
+@pytest.mark.parametrize("draw", ["top_k", "inverse_cdf", "greedy"])
+def test_prompt_history_split_over_slices(draw):
+    """History = prompt ids + generated ids with per-row prompt lengths (repetition for both,
+    frequency and presence for the generated ids only): the slices reach the unsharded
+    sampler's ids, kept sets and statuses."""
+    g = torch.Generator().manual_seed(33)
+    rows, V, L = 16, 30011, 300
+    x = (2.0 * torch.randn(rows, V, generator=g)).to(DEV)
+    h = torch.randint(0, V, (rows, L), generator=g)
+    h[:, 200:] = h[:, :100]
+    h = h.to(DEV)
+    plens = torch.randint(0, L + 1, (rows,), generator=g).to(torch.int32).to(DEV)
+    u = torch.rand(rows, generator=g).to(DEV)
+    pen = dict(temperature=0.9, repetition_penalty=1.25, presence_penalty=0.5, frequency_penalty=0.2)
+    bounds = edges(V, 4, seed=4)
+    if draw == "top_k":
+        knobs = dict(top_k=40, top_p=0.9, **pen)
+        merged, _ = run_sharded(x, bounds, uniforms=u, history=h, history_prompt_lens=plens, **knobs)
+        whole = sample(x, uniforms=u, history=h, history_prompt_lens=plens, check=False, **knobs)
+        assert_same(merged, whole)
+        return
+    res = run_full_sharded(x, bounds, draw, uniforms=u if draw == "inverse_cdf" else None, history=h,
+                           history_prompt_lens=plens, **pen)
+    whole = sample(x, uniforms=u, history=h, history_prompt_lens=plens, greedy=draw == "greedy", check=False, **pen)
+    assert_full_close(res, whole, exact_ids=True)

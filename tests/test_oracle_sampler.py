@@ -91,10 +91,37 @@ def test_penalties_hand_derived():
     assert oracle.penalize(1.0, 3, 1.0, 0.0, 0.5) == -0.5
     assert oracle.penalize(1.0, 3, 1.0, 0.25, 0.5) == -0.75
     assert oracle.penalize(3.0, 2, 1.5, 0.5, 0.25) == 1.0  # 3/1.5 = 2; 2 - 0.5 - 0.5
+    # an id of the prompt only (count 0 among the generated ids): repetition alone
+    assert oracle.penalize(3.0, 0, 1.5, 0.5, 0.25) == 2.0
+    assert oracle.penalize(-3.0, 0, 1.5, 0.5, 0.25) == -4.5
     x, c, rp, pres, freq = 1.2345678, 7, 1.1, 0.3, 0.07
     f32 = np.float32
     want = f32(f32(f32(x) / f32(rp)) - f32(f32(freq) * f32(c))) - f32(pres)
     assert oracle.penalize(x, c, rp, pres, freq) == float(want)
+
+
+def test_prompt_ids_take_repetition_only():
+    # vLLM's rule: repetition over prompt and output ids; frequency and presence count the
+    # generated ids only.  History = prompt [1, 2, 2, 5] + generated [2, 3, 3], T = 1.
+    x = np.array([1.0, 2.0, -1.0, 4.0, 0.5, -2.0, 3.0, 0.25], np.float32)
+    hist = [1, 2, 2, 5, 2, 3, 3]
+    rp, pres, freq = 2.0, 0.5, 0.25
+    z, st = oracle.process_row(x, history=hist, history_prompt_len=4, repetition_penalty=rp,
+                               presence_penalty=pres, frequency_penalty=freq)
+    want = x.copy()
+    want[1] = 2.0 / 2.0                       # prompt only: repetition
+    want[5] = -2.0 * 2.0                      # prompt only, negative logit
+    want[2] = -1.0 * 2.0 - 0.25 * 1 - 0.5     # prompt and generated once
+    want[3] = 4.0 / 2.0 - 0.25 * 2 - 0.5      # generated twice
+    assert st == 0 and np.array_equal(z, want), (z, want)
+    # without the split every entry counts as generated
+    z0, _ = oracle.process_row(x, history=hist, repetition_penalty=rp, presence_penalty=pres, frequency_penalty=freq)
+    assert z0[1] == 1.0 - 0.25 - 0.5 and z0[2] == -2.0 - 0.75 - 0.5 and z0[3] == 2.0 - 0.5 - 0.5
+    # the whole history as prompt: repetition alone everywhere
+    zp, _ = oracle.process_row(x, history=hist, history_prompt_len=7, repetition_penalty=rp, presence_penalty=pres,
+                               frequency_penalty=freq)
+    zr, _ = oracle.process_row(x, history=hist, repetition_penalty=rp)
+    assert np.array_equal(zp, zr)
 
 
 @pytest.mark.parametrize("T", [0.6, 0.7, 1.3, 0.1, 7.77])

@@ -99,6 +99,7 @@ struct Params {
   const int64_t* hist;
   int64_t hstride;
   const int32_t* hlens;
+  const int32_t* plens;  // [rows] or NULL: leading history entries of the prompt (not counted)
   const float* uniforms;
   int64_t* out_ids;
   float* out_lp;
@@ -112,6 +113,8 @@ struct Params {
   float T, rT, rp, pres, freq, top_p, min_p, lmin_f;
   int V, hlen, top_k, greedy, has_pen, unit_T, fast_div, ucap, words, cap;
   int pen_lowers;  // penalties can only lower a logit: rp >= 1, presence >= 0, frequency >= 0
+  int pen_counts;  // the penalty of a history id depends on its count (frequency, or presence
+                   // with prompt ids that count zero)
   // TOPK rows whose candidates fit one wave leave them here for select_kernel:
   // defer_keys[row * DEFER_KEYS + i], defer_count[row] (0: the row was finished in place)
   uint64_t* defer_keys;
@@ -287,7 +290,7 @@ __device__ __forceinline__ float penalize(float x, uint32_t c, const Params& p) 
   x = x > 0.0f ? x / p.rp : x * p.rp;
   float f = p.freq * (float)c;
   x = x - f;
-  x = x - p.pres;
+  if (c > 0) x = x - p.pres;  // c = 0: an id of the prompt only (repetition alone)
   return x;
 }
 
@@ -579,6 +582,7 @@ __device__ __forceinline__ int build_history(const Params& p, int row, const His
   __syncthreads();
   const int hl = hi.hl;
   const int64_t* hr = p.hist + (int64_t)row * p.hstride;
+  const int plen = p.plens ? p.plens[row] : 0;  // entries [0, plen) belong to the prompt
   int bad = 0;
 #pragma unroll
   for (int j = 0; j < HR; ++j) {
@@ -614,18 +618,18 @@ __device__ __forceinline__ int build_history(const Params& p, int row, const His
   int U = 0;
   for (int i = 0; i < NW; ++i) U += m->ri[i];
   __syncthreads();
-  auto count_id = [&](int64_t g) {
+  auto count_id = [&](int64_t g, int idx) {
     const int64_t id = g - id_off;
     if (id >= 0 && id < p.V) {
       const int slot = slot_of(h, (int)id);
-      atomicAdd(&h.cnt2[slot >> 1], 1u << ((slot & 1) * 16));
+      if (idx >= plen) atomicAdd(&h.cnt2[slot >> 1], 1u << ((slot & 1) * 16));
       h.tok[slot] = (uint32_t)id;
     }
   };
 #pragma unroll
   for (int j = 0; j < HR; ++j)
-    if (tid + j * NT < hl) count_id(hi.id[j]);
-  for (int idx = tid + HR * NT; idx < hl; idx += NT) count_id(hr[idx]);
+    if (tid + j * NT < hl) count_id(hi.id[j], tid + j * NT);
+  for (int idx = tid + HR * NT; idx < hl; idx += NT) count_id(hr[idx], idx);
   __syncthreads();
   return U;
 }
@@ -1788,7 +1792,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         __syncthreads();
         // with lowering penalties the stream evaluates history tokens itself and needs
         // their counts only for a frequency penalty
-        if (p.has_pen) U = build_history<NT, HR, EMIT>(p, row, hi, h, m, !p.pen_lowers || p.freq != 0.0f);
+        if (p.has_pen) U = build_history<NT, HR, EMIT>(p, row, hi, h, m, !p.pen_lowers || p.pen_counts);
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
@@ -1882,7 +1886,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
                   if (ok) {
                     if ((hb[k] >> j) & 1u) {
                       if (p.pen_lowers) {
-                        const float z = pen_z(xv, p.freq != 0.0f ? count_of(h, slot_of(h, idx)) : 1u, p);
+                        const float z = pen_z(xv, p.pen_counts ? count_of(h, slot_of(h, idx)) : 1u, p);
                         if (!isfinite(z)) bad = 1;
                         ok = isfinite(z) && z > tau && z >= bnd;
                         if (isfinite(z)) pz = fmaxf(pz, z);
@@ -2898,7 +2902,7 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   // without a frequency penalty need only the membership bitmap.
   pl->topk_nt = TOPK_NT;
   pl->bitmap_only = pl->has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&
-                    d->frequency_penalty == 0.0f;
+                    d->frequency_penalty == 0.0f && !(d->history_prompt_lens && d->presence_penalty != 0.0f);
   if (pl->defer) {
     const int cap256 = k_eff + 256 * TOPK_G;
     const Layout L256 = make_layout<MODE_TOPK, TOPK_G>(V, pl->words, pl->bitmap_only ? 0 : pl->ucap, cap256,
@@ -2960,6 +2964,7 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.hist = d->history;
   p.hstride = d->history_row_stride;
   p.hlens = d->history_lens;
+  p.plens = d->history_prompt_lens;
   p.uniforms = d->uniforms;
   p.out_ids = d->out_ids;
   p.out_lp = d->out_logprob;
@@ -2994,6 +2999,8 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.has_pen = pl.has_pen ? 1 : 0;
   p.pen_lowers = pl.has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&
                  d->frequency_penalty >= 0.0f ? 1 : 0;
+  p.pen_counts = pl.has_pen && (d->frequency_penalty != 0.0f ||
+                                (d->history_prompt_lens && d->presence_penalty != 0.0f)) ? 1 : 0;
   // z = x / T by the three-operation scheme needs x / T normal and finite for
   // 2^-100 <= |x| < 2^100, which holds for T in [2^-20, 2^20]; other temperatures
   // take IEEE division for every element.

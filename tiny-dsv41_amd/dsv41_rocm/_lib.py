@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).with_name("libdsv41hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -62,6 +62,7 @@ class SamplerDesc(ctypes.Structure):
         ("exponentials", ctypes.c_void_p),
         ("exponentials_row_stride", ctypes.c_int64),
         ("replay_ids", ctypes.c_void_p),
+        ("history_prompt_lens", ctypes.c_void_p),
     ]
 
 

@@ -89,6 +89,19 @@ def _rows_in(logits, history, history_lens, temperature, top_k):
     return logits, history, history_lens
 
 
+def _prompt_lens(history_prompt_lens, history, rows, device):
+    """Per-row count of leading history entries that belong to the prompt (int32 on the
+    device), or None."""
+    if history_prompt_lens is None:
+        return None
+    if history is None:
+        raise ValueError("history_prompt_lens requires a history")
+    t = torch.as_tensor(history_prompt_lens).to(device=device, dtype=torch.int32).reshape(-1).contiguous()
+    if t.shape != (rows,):
+        raise ValueError("history_prompt_lens must have one length per row")
+    return t
+
+
 def _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
                frequency_penalty, top_k, top_p, min_p) -> _lib.SamplerDesc:
     desc = _lib.SamplerDesc()
@@ -120,6 +133,7 @@ def sample(
     generator: Optional[torch.Generator] = None,
     history: Optional[torch.Tensor] = None,
     history_lens: Optional[torch.Tensor] = None,
+    history_prompt_lens: Optional[torch.Tensor] = None,
     repetition_penalty: float = 1.0,
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
@@ -133,7 +147,10 @@ def sample(
     """Sample one token per row of ``logits[rows, vocab]`` (fp32 or bf16, on the GPU).
 
     ``history[rows, L]`` (int64, negative = padding) feeds the penalties; ``history_lens``
-    (int32 [rows]) optionally gives ragged lengths.  ``uniforms`` (fp32 [rows] in [0, 1))
+    (int32 [rows]) optionally gives ragged lengths.  With ``history_prompt_lens`` (int32
+    [rows]) the first entries of each row are the prompt's ids and the penalties follow vLLM:
+    repetition for ids of the prompt or the output, frequency and presence for the generated
+    ids only (counted among the entries past the prompt).  ``uniforms`` (fp32 [rows] in [0, 1))
     drive the draw; when omitted they are drawn with ``torch.rand(rows, generator=generator)``
     on the CPU.  With ``check`` the call synchronises and raises the reference's
     ``ValueError`` for non-finite rows, bad uniforms, or a history id at or above the
@@ -171,6 +188,8 @@ def sample(
     status = torch.empty(rows, dtype=torch.int32, device=device)
     desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
                       frequency_penalty, top_k, top_p, min_p)
+    plens = _prompt_lens(history_prompt_lens, history, logits.shape[0], logits.device)
+    desc.history_prompt_lens = _device_ptr(plens)
     desc.uniforms = _device_ptr(uniforms)
     desc.greedy = 1 if greedy else 0
     desc.out_ids = ids.data_ptr()
@@ -241,6 +260,7 @@ def sample_shard(
     temperature: float = 1.0,
     history: Optional[torch.Tensor] = None,
     history_lens: Optional[torch.Tensor] = None,
+    history_prompt_lens: Optional[torch.Tensor] = None,
     repetition_penalty: float = 1.0,
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
@@ -265,6 +285,8 @@ def sample_shard(
     status = torch.empty(rows, dtype=torch.int32, device=device)
     desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
                       frequency_penalty, top_k, top_p, min_p)
+    plens = _prompt_lens(history_prompt_lens, history, logits.shape[0], logits.device)
+    desc.history_prompt_lens = _device_ptr(plens)
     shard = _lib.SamplerShardDesc()
     shard.struct_size = _lib.ctypes.sizeof(_lib.SamplerShardDesc)
     shard.max_candidates = top_k
@@ -341,6 +363,7 @@ def full_shard_states(
     temperature: float = 1.0,
     history: Optional[torch.Tensor] = None,
     history_lens: Optional[torch.Tensor] = None,
+    history_prompt_lens: Optional[torch.Tensor] = None,
     repetition_penalty: float = 1.0,
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
@@ -360,6 +383,8 @@ def full_shard_states(
     states = torch.empty(rows, _lib.FULL_STATE_BYTES // 8, dtype=torch.int64, device=device)
     desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
                       frequency_penalty, 0, 1.0, 0.0)
+    plens = _prompt_lens(history_prompt_lens, history, logits.shape[0], logits.device)
+    desc.history_prompt_lens = _device_ptr(plens)
     d = _lib.SamplerFullShardDesc()
     d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullShardDesc)
     d.sampler = _lib.ctypes.pointer(desc)
@@ -381,7 +406,7 @@ def _gathered(parts, words: int, what: str) -> torch.Tensor:
 
 
 def _shard_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
-                frequency_penalty, vocab_offset, vocab_size, states, shard_index):
+                frequency_penalty, vocab_offset, vocab_size, states, shard_index, history_prompt_lens=None):
     """Descriptor of one slice for the mass and draw steps, with the gathered states."""
     rows, width = logits.shape
     if not (0 <= vocab_offset and vocab_offset + width <= vocab_size):
@@ -393,13 +418,15 @@ def _shard_desc(logits, history, history_lens, temperature, repetition_penalty, 
         raise ValueError("shard_index must name one of the gathered slices")
     desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
                       frequency_penalty, 0, 1.0, 0.0)
+    plens = _prompt_lens(history_prompt_lens, history, logits.shape[0], logits.device)
+    desc.history_prompt_lens = _device_ptr(plens)
     d = _lib.SamplerFullShardDesc()
     d.struct_size = _lib.ctypes.sizeof(_lib.SamplerFullShardDesc)
     d.n_shards = st.shape[0]
     d.vocab_offset, d.vocab_size = vocab_offset, vocab_size
     d.shard_index = shard_index
     d.states = st.data_ptr()
-    return d, desc, st
+    return d, desc, st, plens
 
 
 def full_shard_masses(
@@ -412,6 +439,7 @@ def full_shard_masses(
     temperature: float = 1.0,
     history: Optional[torch.Tensor] = None,
     history_lens: Optional[torch.Tensor] = None,
+    history_prompt_lens: Optional[torch.Tensor] = None,
     repetition_penalty: float = 1.0,
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
@@ -422,8 +450,9 @@ def full_shard_masses(
     over all slices.  Returns int64 ``[rows]`` (the bits of the u64 masses); gather them from
     every slice for :func:`full_shard_draw`.  The exponential race skips this step."""
     logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
-    d, desc, st = _shard_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
-                              frequency_penalty, vocab_offset, vocab_size, states, shard_index)
+    d, desc, st, plens = _shard_desc(logits, history, history_lens, temperature, repetition_penalty,
+                                     presence_penalty, frequency_penalty, vocab_offset, vocab_size, states,
+                                     shard_index, history_prompt_lens)
     masses = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
     d.sampler = _lib.ctypes.pointer(desc)
     d.out_masses = masses.data_ptr()
@@ -448,6 +477,7 @@ def full_shard_draw(
     exponentials: Optional[torch.Tensor] = None,
     history: Optional[torch.Tensor] = None,
     history_lens: Optional[torch.Tensor] = None,
+    history_prompt_lens: Optional[torch.Tensor] = None,
     repetition_penalty: float = 1.0,
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
@@ -464,8 +494,9 @@ def full_shard_draw(
     logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, 0)
     rows = logits.shape[0]
     device = logits.device
-    d, desc, st = _shard_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
-                              frequency_penalty, vocab_offset, vocab_size, states, shard_index)
+    d, desc, st, plens = _shard_desc(logits, history, history_lens, temperature, repetition_penalty,
+                                     presence_penalty, frequency_penalty, vocab_offset, vocab_size, states,
+                                     shard_index, history_prompt_lens)
     ms = None
     if exponentials is not None:
         exponentials = exponentials.to(device=device, dtype=torch.float32)
@@ -565,6 +596,7 @@ def replay_log_probs(
     temperature: float = 1.0,
     history: Optional[torch.Tensor] = None,
     history_lens: Optional[torch.Tensor] = None,
+    history_prompt_lens: Optional[torch.Tensor] = None,
     repetition_penalty: float = 1.0,
     presence_penalty: float = 0.0,
     frequency_penalty: float = 0.0,
@@ -589,6 +621,8 @@ def replay_log_probs(
     status = torch.empty(rows, dtype=torch.int32, device=device)
     desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
                       frequency_penalty, 0, 1.0, 0.0)
+    plens = _prompt_lens(history_prompt_lens, history, logits.shape[0], logits.device)
+    desc.history_prompt_lens = _device_ptr(plens)
     desc.replay_ids = token_ids.data_ptr()
     desc.out_ids, desc.out_logprob, desc.out_status = ids.data_ptr(), lps.data_ptr(), status.data_ptr()
     lib = _lib.load()
