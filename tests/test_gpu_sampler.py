@@ -208,6 +208,24 @@ def test_prompt_history_split(rows, V, knobs):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("rows,dtype,knobs", [
+    (300, torch.float32, dict(top_k=50)),                       # deferred selection
+    (300, torch.bfloat16, dict(top_k=200, top_p=0.9)),
+    (150, torch.float32, dict(top_k=50, top_p=0.95)),           # in place (not deferred)
+])
+def test_top_k_without_min_p_compacts_before_the_selection(rows, dtype, knobs):
+    """Top-k without min-p ends a row with a few hundred candidates; the stream compacts them
+    to the top_k before the final selection, which must give the oracle's ids and kept sets."""
+    g = torch.Generator().manual_seed(rows + 7)
+    V = 151936
+    x = (2.0 * torch.randn(rows, V, generator=g)).to(dtype)
+    x[::5] = (0.01 * torch.randn(len(range(0, rows, 5)), V, generator=g)).to(dtype)  # flat rows
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, 256), generator=g)
+    gpu, ora = run_both(x, u, hist, temperature=0.6, repetition_penalty=1.05, **knobs)
+    assert_exact(gpu, ora)
+
+
 def test_sliced_merge_compacts_under_min_p():
     """Rows of a sliced batch whose slices' lists add up to more than 256 keys go through the
     merge's compaction (the top_k of the union within the min-p bound of its largest key), in

@@ -2012,8 +2012,18 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
     return;
   }
 
+  // Without a min-p bound the buffer can end above what one wave selects from (top-k 50
+  // alone ends near 300 keys).  The final selection keeps a subset of the top_k keys within
+  // the min-p bound of the row maximum, so compacting to those changes only the count,
+  // which then fits the one-wave selection (deferred, or in place) instead of the block sort.
+  int n = count;
+  if (n > DEFER_KEYS && p.top_k > 0 && p.top_k <= DEFER_KEYS && !(m->status & ST_NONFINITE)) {
+    float zm = NEG_INF;
+    for (int i = tid; i < n; i += NT) zm = fmaxf(zm, ckey_z(cand[i]));
+    zm = block_max<NT>(zm, m);
+    n = topk_compact<NT>(cand, n, m, p, zm, tau, tau_key, hist);
+  }
   // final selection over the candidates: one wave when they fit its registers
-  const int n = count;
   if (p.defer && n >= 1 && n <= DEFER_KEYS) {
     // The selection is a serial chain of about 15k cycles in one wave; select_kernel
     // runs it for all rows at once, so this workgroup's slot goes back to streaming.
