@@ -226,6 +226,56 @@ def test_top_k_without_min_p_compacts_before_the_selection(rows, dtype, knobs):
     assert_exact(gpu, ora)
 
 
+@pytest.mark.parametrize("dtype,knobs,prompt", [
+    (torch.float32, dict(temperature=0.6, repetition_penalty=1.05, top_k=1024, top_p=0.98, min_p=0.05), False),
+    (torch.bfloat16, dict(temperature=0.8, presence_penalty=0.5, frequency_penalty=0.2, top_k=50), True),
+    (torch.float32, dict(temperature=1.1, repetition_penalty=0.9, top_k=200, top_p=0.9), False),
+    (torch.float32, dict(temperature=0.7, top_k=1000, min_p=0.02, greedy=True), False),
+])
+def test_large_deferred_batches_match_the_oracle(dtype, knobs, prompt):
+    """2100 rows of 40000 ids (about two workgroups per slot of a full GPU, the deferred
+    selection): Zipf-biased rows, flat rows (every key within min-p, so top_k cuts, or more
+    than 256 survivors end the stream), a NaN and an out-of-vocabulary history id.  Two
+    launches on one workspace give identical outputs."""
+    g = torch.Generator().manual_seed(2100 + int(knobs["top_k"]))
+    rows, V, H = 2100, 40000, 64
+    noise = torch.randn(rows, V, generator=g)
+    perm = torch.argsort(torch.rand(rows, V, generator=g), dim=1)
+    x = noise - 1.1 * torch.log((perm + 1).float())
+    del noise, perm
+    x[::7] = 0.01 * torch.randn(len(range(0, rows, 7)), V, generator=g)  # flat rows
+    x[2000, 39000] = float("nan")
+    x = x.to(dtype)
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, H), generator=g)
+    hist[2050, 5] = V + 3
+    plens = torch.randint(0, H + 1, (rows,), generator=g).to(torch.int32) if prompt else None
+    print(f"case: deferred batch 2100 x 40000 {dtype} knobs={knobs} prompt_lens={prompt}", flush=True)
+    xd, ud, hd = x.to(DEV), u.to(DEV), hist.to(DEV)
+    pd = None if plens is None else plens.to(DEV)
+    runs = []
+    for _ in range(2):
+        res = sample(xd, uniforms=ud, history=hd, history_prompt_lens=pd, check=False, **knobs)
+        torch.cuda.synchronize()
+        runs.append(tuple(t.cpu().numpy() for t in (res.ids, res.logprobs, res.kept, res.status)))
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
+    from concurrent.futures import ThreadPoolExecutor
+    xn, un, hn = x.float().numpy(), u.numpy(), hist.numpy()
+    pn = None if plens is None else plens.numpy()
+    cuts = np.linspace(0, rows, 17).astype(int)
+    with ThreadPoolExecutor(16) as ex:
+        outs = list(ex.map(lambda ab: oracle.sample(
+            xn[ab[0]:ab[1]], uniforms=un[ab[0]:ab[1]], history=hn[ab[0]:ab[1]],
+            history_prompt_lens=None if pn is None else pn[ab[0]:ab[1]], **knobs), zip(cuts[:-1], cuts[1:])))
+    ora = tuple(np.concatenate([o[i] for o in outs]) for i in range(4))
+    assert_exact(runs[0], ora)
+    assert ora[3][2000] != 0
+    penalized = any(k in knobs for k in ("repetition_penalty", "presence_penalty", "frequency_penalty"))
+    assert (ora[3][2050] != 0) == penalized  # the history is read only under a penalty
+    assert (ora[3][:2000] == 0).all()
+
+
 def test_sliced_merge_compacts_under_min_p():
     """Rows of a sliced batch whose slices' lists add up to more than 256 keys go through the
     merge's compaction (the top_k of the union within the min-p bound of its largest key), in

@@ -51,7 +51,8 @@ def _run_both(inp):
     return ws_bytes
 
 
-@pytest.mark.parametrize("first,second", [(("E", 512), ("E", 300)), (("E", 400), ("A", 8))])
+@pytest.mark.parametrize("first,second", [(("E", 512), ("E", 300)), (("E", 400), ("A", 8)),
+                                          (("E", 2200), ("E", 2100))])
 def test_static_scratch_matches_workspace_entry_point(first, second):
     sizes = []
     for name, rows in (first, second):

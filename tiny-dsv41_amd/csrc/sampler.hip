@@ -2012,12 +2012,13 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
     return;
   }
 
-  // Without a min-p bound the buffer can end above what one wave selects from (top-k 50
-  // alone ends near 300 keys).  The final selection keeps a subset of the top_k keys within
-  // the min-p bound of the row maximum, so compacting to those changes only the count,
-  // which then fits the one-wave selection (deferred, or in place) instead of the block sort.
+  // The buffer can end above what one wave selects from: without a min-p bound (top-k 50
+  // alone ends near 300 keys), or with one taken from a running maximum that rose late.  The
+  // final selection keeps a subset of the top_k keys within the min-p bound of the row
+  // maximum, so compacting to those changes only the count, which then fits the one-wave
+  // selection (deferred, or in place) instead of the block sort.
   int n = count;
-  if (n > DEFER_KEYS && p.top_k > 0 && p.top_k <= DEFER_KEYS && !(m->status & ST_NONFINITE)) {
+  if (n > DEFER_KEYS && ((p.top_k > 0 && p.top_k <= DEFER_KEYS) || p.min_p > 0.0f) && !(m->status & ST_NONFINITE)) {
     float zm = NEG_INF;
     for (int i = tid; i < n; i += NT) zm = fmaxf(zm, ckey_z(cand[i]));
     zm = block_max<NT>(zm, m);
