@@ -226,6 +226,34 @@ def test_top_k_without_min_p_compacts_before_the_selection(rows, dtype, knobs):
     assert_exact(gpu, ora)
 
 
+@pytest.mark.parametrize("rows,V,dtype,knobs", [
+    (300, 20011, torch.float32, dict(top_k=50, repetition_penalty=1.3)),                  # deferred, 256 threads
+    (300, 20011, torch.bfloat16, dict(top_k=64, top_p=0.9, repetition_penalty=0.8)),      # raising penalty: gather
+    (300, 20011, torch.float32, dict(top_k=1, presence_penalty=0.5, frequency_penalty=0.3)),
+    (3, 151936, torch.float32, dict(top_k=7, repetition_penalty=1.1)),                    # sliced
+    (5, 151936, torch.bfloat16, dict(top_k=50, top_p=0.95)),                              # sliced, bf16 ties
+])
+def test_top_k_first_batch_threshold(rows, V, dtype, knobs):
+    """Top-k <= 64 without min-p: each wave takes its first threshold from the largest logit
+    of every lane before filtering its first batch.  Rows where that bound meets ties:
+    integer-valued logits (hundreds of elements share each value), a row whose only
+    large logits are history tokens (penalized, so they must not set the bound), rows
+    with +inf and NaN in the first batch, and rows of a constant logit."""
+    g = torch.Generator().manual_seed(rows * 7 + knobs["top_k"])
+    x = 2.0 * torch.randn(rows, V, generator=g)
+    x[0::6] = torch.randint(-5, 6, (len(range(0, rows, 6)), V), generator=g).float()   # ties
+    x[1] = 0.0                                                                            # constant row
+    hist = torch.randint(0, V, (rows, 64), generator=g)
+    x[2, :] = -3.0 + 0.1 * torch.randn(V, generator=g)
+    x[2, hist[2]] = 5.0                                                                   # large history logits
+    if rows > 4:
+        x[3, 17] = float("inf")
+        x[4, 40] = float("nan")
+    u = torch.rand(rows, generator=g)
+    gpu, ora = run_both(x.to(dtype), u, hist, temperature=0.7, **knobs)
+    assert_exact(gpu, ora)
+
+
 @pytest.mark.parametrize("dtype,knobs,prompt", [
     (torch.float32, dict(temperature=0.6, repetition_penalty=1.05, top_k=1024, top_p=0.98, min_p=0.05), False),
     (torch.bfloat16, dict(temperature=0.8, presence_penalty=0.5, frequency_penalty=0.2, top_k=50), True),

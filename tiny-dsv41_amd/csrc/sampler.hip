@@ -1516,6 +1516,50 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&k)[R], int lane) {
   }
 }
 
+// A lower bound of a top_k threshold from one batch of a wave (top_k <= 64 * R): each lane
+// offers its R largest finite logits among the batch's in-range non-history elements; if the
+// wave offers at least top_k of them, tau becomes one float below RN(x_k / T), x_k the
+// top_k-th largest offer.  Those top_k offers are distinct elements with z >= RN(x_k / T)
+// (RN(x / T) is non-decreasing in x), so no element at or below tau ranks in the top_k.
+template <int R, int NT, int PFN, int G>
+__device__ __forceinline__ void seed_tau(const float (&x)[PFN][G], int t0, const Hist& h, const Params& p,
+                                         float& tau) {
+  const int lane = threadIdx.x & 63;
+  float top[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) top[r] = NEG_INF;
+#pragma unroll
+  for (int k = 0; k < PFN; ++k) {
+    const int base = (t0 + k) * NT * G + (int)threadIdx.x * G;
+    const uint32_t pen = p.has_pen && base < p.V ? (h.bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u) : 0u;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float v = x[k][j];
+      if (base + j < p.V && !((pen >> j) & 1u) && isfinite(v)) {
+        if constexpr (R == 1) {
+          top[0] = fmaxf(top[0], v);
+        } else {
+#pragma unroll
+          for (int r = R - 1; r > 0; --r) top[r] = v > top[r - 1] ? top[r - 1] : fmaxf(top[r], v);
+          top[0] = fmaxf(top[0], v);
+        }
+      }
+    }
+  }
+  uint64_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    key[r] = top[r] > NEG_INF ? ((uint64_t)okey(top[r]) << 32) | (uint32_t)(r * 64 + lane) : 0;
+  wave_sort_desc<R>(key, lane);
+  const int pos = p.top_k - 1;
+  uint64_t sel = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r == (pos >> 6)) sel = key[r];
+  const uint64_t kth = __shfl(sel, pos & 63);
+  if (kth != 0) tau = next_down(div_T(okey_inv((uint32_t)(kth >> 32)), p));
+}
+
 // Inclusive prefix of x over positions r*64 + lane; returns the total.
 template <int R>
 __device__ __forceinline__ uint64_t wave_prefix(const uint64_t (&x)[R], uint64_t (&incl)[R], int lane) {
@@ -1828,6 +1872,18 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
           }
           // RN(x/T) is non-decreasing in x: the largest z is the quotient of the largest x
           if (lx > NEG_INF) zmx = fmaxf(zmx, lx / p.T);
+        }
+        // A wave without a top_k threshold (top_k <= 64) takes one before filtering its
+        // first batch: each lane offers its largest finite non-history logit, so the
+        // top_k-th largest offer belongs to top_k distinct elements and the top_k-th
+        // largest z of the row (or shard) is at least its quotient.  tau one float below
+        // that quotient admits every element that can rank in the top_k (tau_key stays 0:
+        // keys then compare only against tau's float).  Without it the first batch fills
+        // the buffer and compacts it several times before any threshold exists.
+        // (256-thread and shard or slice launches: the 512-thread row kernel has no register
+        // left for it at two workgroups per CU)
+        if constexpr (EMIT || NT < TOPK_NT) {
+          if (p.top_k >= 1 && p.top_k <= 64 && !(tau > NEG_INF)) seed_tau<1, NT>(x, t0, h, p, tau);
         }
         wm = uni(fmaxf(wm, wave_max_dpp(zmx)));
         const float bnd = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
