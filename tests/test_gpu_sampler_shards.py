@@ -239,3 +239,41 @@ def test_prompt_history_split_over_slices(draw):
                            history_prompt_lens=plens, **pen)
     whole = sample(x, uniforms=u, history=h, history_prompt_lens=plens, greedy=draw == "greedy", check=False, **pen)
     assert_full_close(res, whole, exact_ids=True)
+
+
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_small_top_k_merge_of_many_lists(shuffle):
+    """top_k <= 64 over more than 64 keys: the merge takes the union's 64 largest keys by
+    bitonic merges of the sorted lists.  Lists handed over in another order (a caller's own
+    gather) fail its sortedness check and take the general merge; both equal the unsharded
+    row and the oracle."""
+    from dsv41_rocm.sampling import ShardCandidates
+
+    g = torch.Generator().manual_seed(640)
+    rows, V = 12, 60000
+    x = 2.0 * torch.randn(rows, V, generator=g)
+    x[3] = 0.01 * torch.randn(V, generator=g)  # flat row: every list full
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, 32), generator=g)
+    knobs = dict(top_k=40, top_p=0.9, repetition_penalty=1.2)
+    bounds = edges(V, 12, 7)
+    xd, ud, hd = x.to(DEV), u.to(DEV), hist.to(DEV)
+    shards = [sample_shard(xd[:, a:b], vocab_offset=a, vocab_size=V, history=hd, top_k=40,
+                           repetition_penalty=1.2) for a, b in zip(bounds[:-1], bounds[1:])]
+    if shuffle:
+        mixed = []
+        for k, sh in enumerate(shards):
+            keys = sh.keys.clone()
+            perm = torch.randperm(keys.shape[1], generator=torch.Generator().manual_seed(k)).to(DEV)
+            for r in range(rows):
+                c = int(sh.counts[r])
+                if c > 1:
+                    keys[r, :c] = keys[r, perm[perm < c]]
+            mixed.append(ShardCandidates(keys, sh.counts, sh.status))
+        shards = mixed
+    print(f"case: 12 lists of top_k=40, shuffled={shuffle}", flush=True)
+    merged = merge_shards(shards, top_k=40, top_p=0.9, uniforms=ud, check=False)
+    whole = sample(xd, uniforms=ud, history=hd, check=False, **knobs)
+    torch.cuda.synchronize()
+    ora = oracle.sample(x.numpy(), uniforms=u.numpy(), history=hist.numpy(), **knobs)
+    assert_same(merged, whole, ora)
