@@ -2039,11 +2039,12 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
                   return z2 > NEG_INF && k2 > tk3 && z2 >= bnd2;
                 }, 1);
         }
-        // A buffer far above its top_k compacts before the next batch instead of when full:
+        // A buffer well above its top_k compacts before the next batch instead of when full:
         // the threshold then rises to the top_k-th of the elements seen so far, and the
         // batches after pass a few elements each instead of a few percent (measured with
-        // top-k 50 alone: 0.886 -> 0.775 ms at E's shape, 32 sliced rows 76.5 -> 50.0 us).
-        if (count > 4 * p.top_k + 256 && t0 + PF < nt)
+        // top-k 50 alone: 0.886 -> 0.745 ms at E's shape, 32 sliced rows 76.5 -> 50.1 us;
+        // the trigger 2 top_k + 128 beat top_k + 192, 4 top_k + 256 and 8 top_k + 256).
+        if (count > 2 * p.top_k + 128 && t0 + PF < nt)
           count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key, hist);
       });
   // NaN and +inf logits passed the filter and flagged the row there; -inf, and a finite
