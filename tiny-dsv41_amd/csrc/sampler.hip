@@ -1354,7 +1354,7 @@ __device__ __forceinline__ uint64_t uni(uint64_t v) {
 
 // The k-th largest of n unique u64 keys in LDS (1 <= k <= n): eight passes of an 8-bit
 // radix selection with u32 bin counts in cnt[256].
-template <int NT>
+template <int NT, bool SHORT = false>
 __device__ __forceinline__ uint64_t kth_largest(const uint64_t* keys, int n, int k, uint32_t* cnt, Misc* m) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   uint64_t prefix = 0, mask = 0;
@@ -1384,6 +1384,7 @@ __device__ __forceinline__ uint64_t kth_largest(const uint64_t* keys, int n, int
           if (acc < target && target <= acc + c[q]) {
             m->bi[0] = 255 - (lane * 4 + q);
             m->bi[1] = (int)(target - acc);
+            if constexpr (SHORT) m->bi[2] = (int)c[q];
           }
           acc += c[q];
         }
@@ -1392,9 +1393,23 @@ __device__ __forceinline__ uint64_t kth_largest(const uint64_t* keys, int n, int
     __syncthreads();
     const int digit = uni(m->bi[0]);
     target = (uint32_t)uni(m->bi[1]);
+    const int in_bin = SHORT ? uni(m->bi[2]) : 0;
     __syncthreads();
     prefix |= (uint64_t)digit << shift;
     mask |= (uint64_t)0xFF << shift;
+    if constexpr (SHORT) {
+      if (in_bin == 1 && shift > 0) {
+        // One key left under the prefix (keys are unique): it is the k-th largest.  One
+        // scan finds it instead of the remaining digit passes (random keys settle in 2-3
+        // bytes).  (Kernels whose occupancy the extra registers would cost keep 8 passes.)
+        for (int i = tid; i < n; i += NT)
+          if ((keys[i] & mask) == prefix) m->bu[0] = keys[i];
+        __syncthreads();
+        const uint64_t key = m->bu[0];
+        __syncthreads();
+        return key;
+      }
+    }
   }
   return prefix;
 }
@@ -1404,7 +1419,7 @@ __device__ __forceinline__ uint64_t kth_largest(const uint64_t* keys, int n, int
 // top_k-th key comes from a radix selection (8 passes of 8 bits over the unique u64
 // keys), and the survivors are compacted in place, in buffer order: about 50x less LDS
 // traffic than sorting the buffer.  The buffer is left unsorted.
-template <int NT>
+template <int NT, bool SHORT = false>
 __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, const Params& p, float mrun, float& tau,
                                             uint64_t& tau_key, uint64_t* hist) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -1422,7 +1437,7 @@ __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, cons
   uint64_t thr = 0;
   if (by_key) {
     if (p.topk_internal && tid == 0) atomicOr(&m->status, ST_FALLBACK);
-    thr = uni(kth_largest<NT>(cand, n, p.top_k, reinterpret_cast<uint32_t*>(hist), m));
+    thr = uni(kth_largest<NT, SHORT>(cand, n, p.top_k, reinterpret_cast<uint32_t*>(hist), m));
     tau_key = thr;
     tau = ckey_z(thr);
   }
@@ -1764,6 +1779,8 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
     p.logits = reinterpret_cast<const TIn*>(p.logits) + v0;
   }
   constexpr int NT = NTK, NW = NT / 64, G = TOPK_G, TILE = NT * G, HR = 4096 / NT;
+  // the radix selection's early exit where its registers cost no occupancy
+  constexpr bool SHORT_SEL = NT < TOPK_NT || (EMIT && VEC && sizeof(TIn) == 4);
   using IdT = std::conditional_t<(NT < TOPK_NT), int32_t, int64_t>;
   constexpr int NE = PF * G + 1;  // elements per thread in one batch round (+1 history slot)
   extern __shared__ __align__(16) unsigned char smem[];
@@ -1810,7 +1827,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
     total = uni(total);
     before = uni(before);
     par ^= 1;
-    if (count + total > p.cap) count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key, hist);
+    if (count + total > p.cap) count = topk_compact<NT, SHORT_SEL>(cand, count, m, p, mblk, tau, tau_key, hist);
     return count + total <= p.cap ? count + before : -1;
   };
   // One insertion round of up to M (<= G) elements per thread; always fits, because
@@ -2045,7 +2062,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         // top-k 50 alone: 0.886 -> 0.745 ms at E's shape, 32 sliced rows 76.5 -> 50.1 us;
         // the trigger 2 top_k + 128 beat top_k + 192, 4 top_k + 256 and 8 top_k + 256).
         if (count > 2 * p.top_k + 128 && t0 + PF < nt)
-          count = topk_compact<NT>(cand, count, m, p, mblk, tau, tau_key, hist);
+          count = topk_compact<NT, SHORT_SEL>(cand, count, m, p, mblk, tau, tau_key, hist);
       });
   // NaN and +inf logits passed the filter and flagged the row there; -inf, and a finite
   // x whose x / T or penalized value could overflow, show in |x|: rare, so such rows
@@ -2101,7 +2118,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
     float zm = NEG_INF;
     for (int i = tid; i < n; i += NT) zm = fmaxf(zm, ckey_z(cand[i]));
     zm = block_max<NT>(zm, m);
-    n = topk_compact<NT>(cand, n, m, p, zm, tau, tau_key, hist);
+    n = topk_compact<NT, SHORT_SEL>(cand, n, m, p, zm, tau, tau_key, hist);
   }
   // final selection over the candidates: one wave when they fit its registers
   if (p.defer && n >= 1 && n <= DEFER_KEYS) {
