@@ -229,7 +229,9 @@ typedef struct dsv41_sampler_merge_desc {
   int32_t rows;
   int32_t n_shards;
   int32_t max_candidates;  /* keys per row and slice in `keys` */
-  const uint64_t* keys;    /* [n_shards, rows, max_candidates] */
+  const uint64_t* keys;    /* [n_shards, rows, max_candidates], each list in any order; lists
+                              sorted descending, as dsv41_sampler_shard_run leaves them, take
+                              a faster merge when top_k <= 64 */
   const int32_t* counts;   /* [n_shards, rows] */
   const int32_t* status;   /* [n_shards, rows] */
   const float* uniforms;   /* [rows]; may be NULL only when greedy != 0 */
