@@ -212,10 +212,13 @@ def test_prompt_history_split(rows, V, knobs):
     (300, torch.float32, dict(top_k=50)),                       # deferred selection
     (300, torch.bfloat16, dict(top_k=200, top_p=0.9)),
     (150, torch.float32, dict(top_k=50, top_p=0.95)),           # in place (not deferred)
+    (300, torch.float32, dict(top_k=40, min_p=0.002)),          # weak min-p: compactions under both bounds
+    (300, torch.bfloat16, dict(top_k=1)),
 ])
 def test_top_k_without_min_p_compacts_before_the_selection(rows, dtype, knobs):
-    """Top-k without min-p ends a row with a few hundred candidates; the stream compacts them
-    to the top_k before the final selection, which must give the oracle's ids and kept sets."""
+    """Top-k with no or a weak min-p bound: the buffer compacts in mid-stream once it holds
+    more than 2 top_k + 128 keys, and rows end with a few hundred candidates that compact to
+    the top_k before the final selection; ids and kept sets must be the oracle's."""
     g = torch.Generator().manual_seed(rows + 7)
     V = 151936
     x = (2.0 * torch.randn(rows, V, generator=g)).to(dtype)
