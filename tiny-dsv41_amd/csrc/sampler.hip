@@ -1603,16 +1603,36 @@ __device__ __forceinline__ uint64_t wave_prefix(const uint64_t (&x)[R], uint64_t
   return carry;
 }
 
+// Descending order of n <= 64 unique keys, one per lane (lanes >= n hold 0, below every
+// key), by rank: each lane counts the keys in buf[0, n) above its own and places its key
+// there; buf then holds the sorted keys and each lane reads back its position.  The
+// result is the bitonic network's, in about 2n LDS broadcast reads instead of 21
+// exchange steps (the final selections of typical rows hold a few keys).
+__device__ __forceinline__ uint64_t wave_rank_desc(uint64_t v, uint64_t* buf, int n, int lane) {
+  int rank = 0;
+  for (int i = 0; i < n; ++i) rank += buf[i] > v ? 1 : 0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < n) buf[rank] = v;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return lane < n ? buf[lane] : 0;
+}
+
 // Final selection of the TOPK kernel by one wave when 1 <= n <= 64*R candidates: the
 // same decisions as the workgroup path (min-p, top-k, top-p over exact integer masses,
-// inverse-CDF draw in vocabulary order), with every step in registers.
+// inverse-CDF draw in vocabulary order), with every step in registers.  cand (LDS, this
+// wave's to overwrite) holds the keys; with R = 1 the two sorts go by rank through it.
 template <int R>
-__device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, const uint64_t* cand, int n, float u) {
+__device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, uint64_t* cand, int n, float u) {
   const int lane = threadIdx.x & 63;
   uint64_t k[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) k[r] = r * 64 + lane < n ? cand[r * 64 + lane] : 0;  // 0 is below every key
-  wave_sort_desc<R>(k, lane);
+  if constexpr (R == 1) k[0] = wave_rank_desc(k[0], cand, n, lane);
+  else wave_sort_desc<R>(k, lane);
   const uint64_t k0 = __shfl(k[0], 0);
   const float zmax = ckey_z(k0);
   int el = 0;
@@ -1656,7 +1676,15 @@ __device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, co
 #pragma unroll
     for (int r = 0; r < R; ++r)
       k2[r] = r * 64 + lane < n_keep ? ~(((uint64_t)ckey_idx(k[r]) << 32) | (k[r] >> 32)) : 0;
-    wave_sort_desc<R>(k2, lane);
+    if constexpr (R == 1) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      cand[lane] = k2[0];  // (the sorted keys stay in k)
+      k2[0] = wave_rank_desc(k2[0], cand, n_keep, lane);
+    } else {
+      wave_sort_desc<R>(k2, lane);
+    }
     const uint64_t t = draw_target(u, S);
     uint64_t w[R], cum[R];
 #pragma unroll
