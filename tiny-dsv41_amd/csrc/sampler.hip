@@ -2727,21 +2727,31 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int ro
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int row = blockIdx.x * SEL_WAVES + wid;
   if (row >= rows) return;
+  // The row's count, status, uniform and first 64 key slots load together (one round trip
+  // instead of three; all DEFER_KEYS slots of a row are allocated, and those past its
+  // count are not used).  Most rows hold fewer than 64 keys.
+  const uint64_t* keys = p.defer_keys + (int64_t)row * DEFER_KEYS;
+  const uint64_t first = keys[lane];
   const int n = p.defer_count[row];
+  const int st0 = p.out_status[row];
+  const float u0 = p.greedy ? 0.0f : p.uniforms[row];
   if (n < 1 || n > DEFER_KEYS) return;
   Misc* m = &ms[wid];
-  if (lane == 0) m->status = p.out_status[row];
+  if (lane == 0) m->status = st0;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const float u = row_uniform(p, row, m);
-  const uint64_t* keys = p.defer_keys + (int64_t)row * DEFER_KEYS;
+  float u = u0;  // as row_uniform
+  if (!p.greedy && !(u0 >= 0.0f && u0 < 1.0f)) {
+    atomicOr(&m->status, ST_BAD_UNIFORM);
+    u = 0.0f;
+  }
   constexpr int RK = DEFER_KEYS / 64;
   uint64_t k[RK];
   uint64_t kmax = 0;
 #pragma unroll
   for (int r = 0; r < RK; ++r) {
-    k[r] = r * 64 + lane < n ? keys[r * 64 + lane] : 0;  // 0 is below every key
+    k[r] = r * 64 + lane < n ? (r == 0 ? first : keys[r * 64 + lane]) : 0;  // 0 is below every key
     kmax = k[r] > kmax ? k[r] : kmax;
   }
   // the largest key: its z is the row maximum the selection measures min-p against
