@@ -81,13 +81,27 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
 }
 
-// inclusive prefix sums across the 64 lanes
+// inclusive prefix sums across the 64 lanes (all lanes active).  Integer sums are exact in
+// any order, so the integer scans go by DPP: shifts of 1, 2, 4 and 8 lanes within each
+// 16-lane row (lanes whose source lies before the row read 0), then row 0's total into
+// row 1 and row 2's into row 3 (row_bcast:15), then lane 31's into rows 2 and 3
+// (row_bcast:31): no LDS crossbar round trips.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_scan_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint64_t dpp_scan_u64(uint64_t v) {
+  return ((uint64_t)dpp_scan_u32<CTRL, ROWS>((uint32_t)(v >> 32)) << 32) | dpp_scan_u32<CTRL, ROWS>((uint32_t)v);
+}
 __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    uint64_t t = __shfl_up(v, o);
-    if (lane >= o) v += t;
-  }
+  (void)lane;
+  v += dpp_scan_u64<0x111>(v);        // row_shr:1
+  v += dpp_scan_u64<0x112>(v);        // row_shr:2
+  v += dpp_scan_u64<0x114>(v);        // row_shr:4
+  v += dpp_scan_u64<0x118>(v);        // row_shr:8
+  v += dpp_scan_u64<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_scan_u64<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
   return v;
 }
 __device__ __forceinline__ double wave_incl_scan_d(double v, int lane) {
