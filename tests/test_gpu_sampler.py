@@ -604,3 +604,31 @@ def test_custom_op_matches_wrapper():
     ref = sample(x, uniforms=u, history=h, **k)
     assert torch.equal(ids, ref.ids) and torch.equal(lps, ref.logprobs)
     assert torch.equal(kept, ref.kept) and torch.equal(st, ref.status)
+
+
+@pytest.mark.parametrize("V,dtype,knobs", [
+    ((1 << 21) - 1, torch.float32, dict()),                        # full vocabulary, exact draw
+    ((1 << 21) - 1, torch.bfloat16, dict(greedy=True)),
+    ((1 << 21) - 1, torch.float32, dict(top_k=50, top_p=0.95)),
+    ((1 << 21) - 1, torch.float32, dict(top_p=0.9)),
+    ((1 << 21) - 1, torch.bfloat16, dict(min_p=0.05)),
+    ((1 << 21) - 1, torch.float32, dict(top_k=3000)),               # above the TOPK kernel's bound
+    (600_011, torch.float32, dict(top_k=50, top_p=0.95, repetition_penalty=1.1)),
+    (600_011, torch.bfloat16, dict(min_p=0.05, presence_penalty=0.3)),
+    (600_011, torch.float32, dict(frequency_penalty=0.2)),
+])
+def test_largest_vocabulary(V, dtype, knobs):
+    """Rows of 2^21 - 1 ids, the largest vocabulary the sampler takes (and of 600,011 ids with
+    penalties, whose tables must fit on chip): a flat row, whose exact masses sum to
+    (2^21 - 1) * 2^43 just below 2^64 at the largest size, a row whose maximum is the last id,
+    which is also in its history, and two random rows."""
+    g = torch.Generator().manual_seed(21)
+    x = 3.0 * torch.randn(4, V, generator=g)
+    x[1] = 0.0                                   # flat
+    x[2, V - 1] = 20.0                           # maximum at the last id
+    u = torch.rand(4, generator=g)
+    hist = torch.randint(0, V, (4, 32), generator=g)
+    hist[2, 0] = V - 1
+    gpu, ora = run_both(x.to(dtype), None if knobs.get("greedy") else u, hist, temperature=0.8, **knobs)
+    assert_exact(gpu, ora)
+    assert (ora[3] == 0).all()
