@@ -161,6 +161,7 @@ struct Misc {
   int U;
   float tau;
   uint64_t tau_key;
+  int unsorted;  // merge_kernel: some list is not in descending order
 };
 
 struct Layout {
@@ -2866,7 +2867,7 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
     const int lane = tid & 63;
     const int* cnt = reinterpret_cast<const int*>(hist);
     const int* off = cnt + 256;
-    if (tid == 0) m->bi[2] = 0;
+    if (tid == 0) m->unsorted = 0;
     __syncthreads();
     uint64_t best = 0;  // 0 is below every key
     int unsorted = 0;
@@ -2876,9 +2877,9 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
       unsorted |= b > __shfl_down(b, 1) ? 1 : 0;                           // (lane 63 compares with itself)
       best = wave_merge_top64(best, b, lane);
     }
-    if (__ballot(unsorted) && lane == 0) atomicOr(&m->bi[2], 1);
+    if (__ballot(unsorted) && lane == 0) atomicOr(&m->unsorted, 1);
     __syncthreads();  // every list read: cand takes the waves' results
-    if (m->bi[2] == 0) {
+    if (m->unsorted == 0) {
       cand[wid * 64 + lane] = best;
       for (int half = NW / 2; half >= 1; half >>= 1) {
         __syncthreads();
