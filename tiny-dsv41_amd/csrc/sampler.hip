@@ -68,6 +68,12 @@ constexpr int TOPP_BIN_BASE = 100 << 7;        // octave 0 is [2^-27, 2^-26); sm
 constexpr int TOPP_CAP = 4096;                 // list / boundary-bin tokens topp_kernel holds
 static_assert(TOPP_CAP <= TOPP_BINS, "the boundary bin's tokens from the list go to the bins' space");
 constexpr size_t LDS_LIMIT = 160 * 1024;
+// Cache policy of the row streams: nt (non-temporal).  A pass reads each logit and history
+// id once, so its lines should not take L2 or Infinity Cache space from data that is
+// reused.  At E (4096 x 151936 fp32) this took a launch from 483 to 437 us, and top-p
+// (three reads of a row) is unchanged.
+constexpr int STREAM_CPOL = 2;
+constexpr int FULL_CPOL = 0;  // full_kernel's exact draw re-reads each row: default caching
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr uint32_t NEG_INF_BITS = 0xFF800000u;
@@ -557,7 +563,7 @@ __device__ __forceinline__ void load_history(const Params& p, int row, HistIds<H
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(hr, (uint32_t)p.hstride * 8u);
 #pragma unroll
   for (int j = 0; j < HR; ++j) {
-    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(tid + j * NT) * 8u, 0, 0);
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)(tid + j * NT) * 8u, 0, STREAM_CPOL);
     const int64_t g = (int64_t)(((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x);
     if constexpr (sizeof(IdT) == 4)
       hi.id[j] = g < 0 ? -1 : (g > (int64_t)INT32_MAX ? INT32_MAX : (int32_t)g);
@@ -642,28 +648,28 @@ struct Raw {
   uint32_t w[WORDS];
 };
 
-template <typename TIn, int G, bool VEC>
+template <typename TIn, int G, bool VEC, int CPOL = STREAM_CPOL>
 __device__ __forceinline__ void load_group(Raw<TIn, G>& r, __amdgpu_buffer_rsrc_t rs, int base) {
   constexpr int WORDS = Raw<TIn, G>::WORDS;
   const uint32_t off = (uint32_t)base * (uint32_t)sizeof(TIn);
   if constexpr (VEC && WORDS == 4) {
-    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, CPOL);
     r.w[0] = (uint32_t)v.x;
     r.w[1] = (uint32_t)v.y;
     r.w[2] = (uint32_t)v.z;
     r.w[3] = (uint32_t)v.w;
   } else if constexpr (VEC && WORDS == 2) {
-    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, CPOL);
     r.w[0] = (uint32_t)v.x;
     r.w[1] = (uint32_t)v.y;
   } else if constexpr (sizeof(TIn) == 4) {
 #pragma unroll
-    for (int j = 0; j < G; ++j) r.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, off + 4 * j, 0, 0);
+    for (int j = 0; j < G; ++j) r.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, off + 4 * j, 0, CPOL);
   } else {
 #pragma unroll
     for (int i = 0; i < WORDS; ++i) {
-      const uint32_t lo = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 4 * i, 0, 0);
-      const uint32_t hi = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 4 * i + 2, 0, 0);
+      const uint32_t lo = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 4 * i, 0, CPOL);
+      const uint32_t hi = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off + 4 * i + 2, 0, CPOL);
       r.w[i] = lo | (hi << 16);
     }
   }
@@ -811,7 +817,7 @@ __device__ __forceinline__ void landed(const HistIds<HR, IdT>& hi) {
 // LOWERING: the caller meets history tokens in the stream itself when p.pen_lowers is
 // set, and the gather is off then (a compile-time switch: an extra runtime flag costs
 // full_kernel the scalar registers that keep it at two workgroups per CU).
-template <typename TIn, int G, int NT, bool VEC, bool LOWERING, class Setup, class Batch>
+template <typename TIn, int G, int NT, bool VEC, bool LOWERING, int CPOL = STREAM_CPOL, class Setup, class Batch>
 __device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc_t rs, const Hist& h,
                                            Setup setup, Batch batch) {
   constexpr int TILE = NT * G;
@@ -819,7 +825,7 @@ __device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc
   const int nt = (p.V + TILE - 1) / TILE;
   Raw<TIn, G> A[PF], B[PF];
 #pragma unroll
-  for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(A[k], rs, k * TILE + tid * G);
+  for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC, CPOL>(A[k], rs, k * TILE + tid * G);
   const int U = setup();
   auto gather = [&](int t0, int& s0, int& n) -> float {
     if (!p.has_pen || (LOWERING && p.pen_lowers)) {
@@ -835,12 +841,12 @@ __device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc
   float gA = gather(0, sA, nA), gB = 0.0f;
   for (int t0 = 0; t0 < nt; t0 += 2 * PF) {
 #pragma unroll
-    for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(B[k], rs, (t0 + PF + k) * TILE + tid * G);
+    for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC, CPOL>(B[k], rs, (t0 + PF + k) * TILE + tid * G);
     gB = gather(t0 + PF, sB, nB);
     batch(t0, nt, A, sA, nA, gA);
     if (t0 + PF >= nt) break;
 #pragma unroll
-    for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC>(A[k], rs, (t0 + 2 * PF + k) * TILE + tid * G);
+    for (int k = 0; k < PF; ++k) load_group<TIn, G, VEC, CPOL>(A[k], rs, (t0 + 2 * PF + k) * TILE + tid * G);
     gA = gather(t0 + 2 * PF, sA, nA);
     batch(t0 + PF, nt, B, sB, nB, gB);
   }
@@ -930,7 +936,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   constexpr int TILE = NT * G;
   int bad = 0;
   int U = 0;
-  stream_row<TIn, G, NT, VEC, false>(
+  stream_row<TIn, G, NT, VEC, false, FULL_CPOL>(
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
@@ -1056,9 +1062,9 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     for (int t = 0; t < nt; ++t) {
       const int base = t * TILE + tid * G;
       Raw<TIn, G> r;
-      load_group<TIn, G, VEC>(r, rs, base);
+      load_group<TIn, G, VEC, FULL_CPOL>(r, rs, base);
       Raw<float, G> er;
-      load_group<float, G, false>(er, re, base);
+      load_group<float, G, false, FULL_CPOL>(er, re, base);
       float x[G], z[G];
       unpack(r, x);
       int dummy = 0;
@@ -1172,9 +1178,9 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   if (exact) {
     const int nt = (p.V + TILE - 1) / TILE;
     Raw<TIn, G> R0, R1;
-    load_group<TIn, G, VEC>(R0, rs, tid * G);
+    load_group<TIn, G, VEC, FULL_CPOL>(R0, rs, tid * G);
     for (int t = 0; t < nt; ++t) {
-      load_group<TIn, G, VEC>(R1, rs, (t + 1) * TILE + tid * G);  // past the row: zeros
+      load_group<TIn, G, VEC, FULL_CPOL>(R1, rs, (t + 1) * TILE + tid * G);  // past the row: zeros
       const int base = t * TILE + tid * G;
       float x[G], z[G];
       unpack(R0, x);
@@ -1261,7 +1267,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     auto chunk_z = [&](int c, float(&z)[G]) {
       const int base = c * 64 * G + lane * G;
       Raw<TIn, G> r;
-      load_group<TIn, G, VEC>(r, rs, base);
+      load_group<TIn, G, VEC, FULL_CPOL>(r, rs, base);
       float x[G];
       unpack(r, x);
       int dummy = 0;
