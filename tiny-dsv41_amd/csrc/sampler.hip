@@ -1953,7 +1953,9 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         if constexpr (EMIT || NT < TOPK_NT) {
           if (p.top_k >= 1 && p.top_k <= 64 && !(tau > NEG_INF)) seed_tau<1, NT>(x, t0, h, p, tau);
         }
-        wm = uni(fmaxf(wm, wave_max_dpp(zmx)));
+        // (skipped when no lane holds a finite value: the maximum is then unchanged; the
+        // test costs the unaligned-row instantiations their fourth wave per SIMD)
+        if (!VEC || __ballot(zmx > NEG_INF)) wm = uni(fmaxf(wm, wave_max_dpp(zmx)));
         const float bnd = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
         if (!(tau == c_tau && bnd == c_bnd)) {
           c_tau = tau;
@@ -1976,6 +1978,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
             bal[k * G + j] = __ballot(!(x[k][j] < th));
             any |= bal[k * G + j];
           }
+        uint32_t wn = 0;  // the wave's passers, counted where they are decided
         if (any) {
           // Passers are rare once the thresholds settle.  Positions past the row drop
           // out and a non-finite logit flags the row.  The passers' z replaces x in
@@ -2026,14 +2029,12 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
                   }
                 }
                 bal[e] = __ballot(ok);
+                wn += (uint32_t)__popcll(bal[e]);
               }
             }
           }
           wm = uni(fmaxf(wm, wave_max_dpp(pz)));
         }
-        uint32_t wn = 0;
-#pragma unroll
-        for (int e = 0; e < NE - 1; ++e) wn += (uint32_t)__popcll(bal[e]);
         const uint64_t kg = ckey(zg, tg);
         bal[NE - 1] = __ballot(zg > NEG_INF && kg > tk && zg >= bnd);
         wn += (uint32_t)__popcll(bal[NE - 1]);
