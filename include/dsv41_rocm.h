@@ -63,6 +63,10 @@ extern "C" {
 #define DSV41_STATUS_BAD_UNIFORM 4 /* uniform outside [0, 1) (row drawn with u = 0)    */
 #define DSV41_STATUS_RATIO_ZERO 8  /* Token-TIS raw weight exp(old - behaviour) == 0   */
 #define DSV41_STATUS_BAD_TARGET 16 /* a replay id was outside [0, vocab) (lp = NaN)    */
+#define DSV41_STATUS_BAD_SLICES 32 /* full-vocabulary draw over slices: the gathered    */
+                                   /* masses place the target in no slice's own masses  */
+                                   /* (states, masses and draw step from other inputs); */
+                                   /* id -1, lp NaN                                     */
 
 /*
  * Row sampler.  For each row r of logits[rows, vocab]:

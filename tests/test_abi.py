@@ -369,3 +369,31 @@ def test_sampler_full_finish_rejects_bad_descriptors(kw, code, msg):
         setattr(d, k, v)
     assert lib.dsv41_sampler_full_finish_run(ctypes.byref(d), None) == code
     assert msg in _lib.last_error()
+
+
+def _integration_stub():
+    """The first python block of INTEGRATION.md's ctypes section, the binding a maintainer copies."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    section = text.split("## 1. The ctypes binding", 1)[1]
+    return section.split("```python\n", 1)[1].split("```", 1)[0]
+
+
+def test_integration_stub_matches_the_binding(monkeypatch):
+    # The stub loads the library by a path relative to the repository root, checks the ABI
+    # version and the sampler descriptor's size, and binds every entry point it names.
+    monkeypatch.chdir(ROOT)
+    ns = {}
+    exec(compile(_integration_stub(), "INTEGRATION.md", "exec"), ns)
+    pairs = {"SamplerDesc": _lib.SamplerDesc, "LogprobDesc": _lib.LogprobDesc,
+             "LogprobGradDesc": _lib.LogprobGradDesc, "GrpoDesc": _lib.GrpoDesc,
+             "TokenTisDesc": _lib.TokenTisDesc}
+    for name, cls in pairs.items():
+        stub = ns[name]
+        assert [f for f, _ in stub._fields_] == [f for f, _ in cls._fields_], name
+        assert ctypes.sizeof(stub) == ctypes.sizeof(cls), name
+        for fname, _ in cls._fields_:
+            assert getattr(stub, fname).offset == getattr(cls, fname).offset, (name, fname)
+    assert ns["lib"].dsv41_abi_version() == _lib.ABI_VERSION
+    bound = set(re.findall(r"\blib\.(dsv41_[a-z_]+)\.", _integration_stub()))
+    assert bound <= set(_lib.EXPORTS)
+    assert "dsv41_sampler_run_static" in bound

@@ -241,6 +241,38 @@ def test_prompt_history_split_over_slices(draw):
     assert_full_close(res, whole, exact_ids=True)
 
 
+def test_masses_that_no_slice_holds_flag_the_row():
+    """The inverse-CDF draw step places the token against masses gathered from every slice.
+    When they come from other inputs than the draw step's (here slice 0's mass is inflated a
+    hundredfold), the slice they name as the owner cannot hold the target in its own masses:
+    no id is placed, and the finish flags the row instead of returning the slice's first id."""
+    g = torch.Generator().manual_seed(11)
+    rows, V = 16, 4096
+    x = torch.randn(rows, V, generator=g).to(DEV)
+    u = torch.full((rows,), 0.5).to(DEV)
+    bounds = [0, V // 2, V]
+    slices = list(enumerate(zip(bounds[:-1], bounds[1:])))
+    print(f"case: mismatched slice masses rows={rows} V={V}", flush=True)
+    states = [full_shard_states(x[:, a:b], vocab_offset=a, vocab_size=V) for _, (a, b) in slices]
+    masses = [full_shard_masses(x[:, a:b], states, shard_index=i, vocab_offset=a, vocab_size=V)
+              for i, (a, b) in slices]
+    # masses of 2^43 per unit of exp(z - M): a 2048-id half stays far below 2^63 / 100
+    assert int(masses[0].max()) < (1 << 56)
+    bad = [masses[0] * 100, masses[1]]
+    picks = [full_shard_draw(x[:, a:b], states, bad, shard_index=i, vocab_offset=a, vocab_size=V, uniforms=u)
+             for i, (a, b) in slices]
+    res = full_shard_finish(states, picks, vocab_size=V, draw="inverse_cdf", uniforms=u, check=False)
+    assert bool((res.status & 32 != 0).all())
+    assert bool((res.ids == -1).all()) and bool(torch.isnan(res.logprobs).all())
+    with pytest.raises(ValueError, match="slice masses"):
+        full_shard_finish(states, picks, vocab_size=V, draw="inverse_cdf", uniforms=u)
+    good = [full_shard_draw(x[:, a:b], states, masses, shard_index=i, vocab_offset=a, vocab_size=V, uniforms=u)
+            for i, (a, b) in slices]
+    ok = full_shard_finish(states, good, vocab_size=V, draw="inverse_cdf", uniforms=u)
+    whole = sample(x, uniforms=u)
+    assert torch.equal(ok.ids, whole.ids) and bool((ok.status == 0).all())
+
+
 @pytest.mark.parametrize("shuffle", [False, True])
 def test_small_top_k_merge_of_many_lists(shuffle):
     """top_k <= 64 over more than 64 keys: the merge takes the union's 64 largest keys by

@@ -71,3 +71,54 @@ def test_static_scratch_rejects_batches_above_its_size():
     rc = _lib.load().dsv41_sampler_run_static(ctypes.byref(_desc(inp, outs)),
                                              torch.cuda.current_stream(DEV).cuda_stream)
     assert rc == _lib.E_UNSUPPORTED and "static maximum" in _lib.last_error()
+
+
+def _flat_rows_inputs(rows, knobs, seed):
+    """fp32 rows of config E's vocabulary; every third row flat, so that a min-p bound keeps
+    the whole row (more survivors than the internal bound: those rows take the fallback)."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(rows, 151936, generator=g)
+    logits[::3] = 0.0
+    return dict(logits=logits.to(DEV), history=None, uniforms=torch.rand(rows, generator=g).to(DEV), knobs=knobs)
+
+
+def test_static_scratch_top_p_alone_then_min_p_fallback_rows():
+    # top-p alone on 32 rows keeps one fp32 z row per row in the scratch (19.4 MB); min-p
+    # alone then runs the internal top-k bound, and its flat rows go to generic_kernel,
+    # whose z rows follow in the same array
+    sizes = []
+    for rows, knobs, seed in ((32, dict(top_p=0.9, temperature=0.8), 1), (12, dict(min_p=0.05), 2)):
+        print(f"case: dsv41_sampler_run_static rows={rows} knobs={knobs}", flush=True)
+        sizes.append(_run_both(_flat_rows_inputs(rows, knobs, seed)))
+    assert sizes[1] < sizes[0]
+
+
+def test_static_scratch_replays_under_graph_capture():
+    # The entry point allocates and clears nothing, so a captured launch replays as is.
+    lib = _lib.load()
+    inp = workloads.sampler_inputs("E", rows=300, device=DEV)
+    rows = 300
+    ref, got = _outs(rows), _outs(rows)
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    _lib.check(lib.dsv41_sampler_run_static(ctypes.byref(_desc(inp, ref)), stream))
+    torch.cuda.synchronize()
+    dg = _desc(inp, got)
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(side):  # warm-up off the default stream, as capture requires
+        _lib.check(lib.dsv41_sampler_run_static(ctypes.byref(dg), side.cuda_stream))
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print("case: dsv41_sampler_run_static under graph capture, E 300 rows", flush=True)
+    with torch.cuda.graph(graph):
+        rc = lib.dsv41_sampler_run_static(ctypes.byref(dg), torch.cuda.current_stream(DEV).cuda_stream)
+    _lib.check(rc)
+    for _ in range(3):
+        for t in got:
+            t.fill_(-5)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b)

@@ -31,6 +31,7 @@
 // This file is compiled with -ffp-contract=off: each operation rounds as written.
 
 #include <math.h>
+#include <limits.h>
 #include <string.h>
 
 #include <mutex>
@@ -83,6 +84,7 @@ constexpr int ST_NONFINITE = DSV41_STATUS_NONFINITE;
 constexpr int ST_BAD_HISTORY = DSV41_STATUS_BAD_HISTORY;
 constexpr int ST_BAD_UNIFORM = DSV41_STATUS_BAD_UNIFORM;
 constexpr int ST_BAD_TARGET = DSV41_STATUS_BAD_TARGET;
+constexpr int ST_BAD_SLICES = DSV41_STATUS_BAD_SLICES;
 constexpr int ST_RECHECK = 1 << 30;  // internal to topk_kernel: re-check every element of the row
 constexpr int ST_FALLBACK = 1 << 29; // internal: an internal-k TOPK row needs generic_kernel
 
@@ -135,6 +137,10 @@ struct Params {
   // cut its min-p survivors at it is flagged ST_FALLBACK and redone by generic_kernel,
   // which then runs only on flagged rows (only_flagged)
   int topk_internal, only_flagged;
+  // TOPK buffer size above which a batch compacts mid-stream (2 top_k + 128); none under
+  // the internal bound, where a compaction against the running maximum could cut min-p
+  // survivors that the final bound keeps
+  int mid_trigger;
   // full-vocabulary draw over slices (DRAW_STATE / DRAW_SHARD_*): states [n_shards, nrows]
   const dsv41_full_state* sh_states;
   dsv41_full_state* sh_out_states;
@@ -1338,7 +1344,10 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
         st.reserved = 0;
         p.sh_out_states[row] = st;
       } else if constexpr (DRAW == DRAW_SHARD_CDF) {
-        p.sh_out_picks[row] = dsv41_full_pick{tok + p.voff, ztok, 0.0f};
+        // The owning slice's own masses must hold the target; when they do not (masses
+        // gathered from other knobs, history or logits than this step's), no id is placed
+        // and the finish flags the row.
+        p.sh_out_picks[row] = dsv41_full_pick{m->bi[0] >= 0 ? tok + p.voff : -1, ztok, 0.0f};
       } else {
         const float lp = (float)(((double)ztok - (double)M) - log(S));
         write_result(p, row, m, tok, lp, p.V);
@@ -1443,7 +1452,10 @@ __device__ __forceinline__ int topk_compact(uint64_t* cand, int n, Misc* m, cons
   const bool by_key = el >= p.top_k && p.top_k > 0;
   uint64_t thr = 0;
   if (by_key) {
-    if (p.topk_internal && tid == 0) atomicOr(&m->status, ST_FALLBACK);
+    // Under the internal bound, el == top_k keys inside the bound all survive, which is
+    // the min-p compaction itself; only more than top_k of them send the row to the
+    // fallback (as in block_final).
+    if (p.topk_internal && el > p.top_k && tid == 0) atomicOr(&m->status, ST_FALLBACK);
     thr = uni(kth_largest<NT, SHORT>(cand, n, p.top_k, reinterpret_cast<uint32_t*>(hist), m));
     tau_key = thr;
     tau = ckey_z(thr);
@@ -2097,7 +2109,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         // batches after pass a few elements each instead of a few percent (measured with
         // top-k 50 alone: 0.886 -> 0.745 ms at E's shape, 32 sliced rows 76.5 -> 50.1 us;
         // the trigger 2 top_k + 128 beat top_k + 192, 4 top_k + 256 and 8 top_k + 256).
-        if (count > 2 * p.top_k + 128 && t0 + PF < nt)
+        if (count > p.mid_trigger && t0 + PF < nt)
           count = topk_compact<NT, SHORT_SEL>(cand, count, m, p, mblk, tau, tau_key, hist);
       });
   // NaN and +inf logits passed the filter and flagged the row there; -inf, and a finite
@@ -2967,16 +2979,20 @@ __global__ __launch_bounds__(256) void full_finish_kernel(dsv41_sampler_full_fin
   } else {
     const float u = d.uniforms[row];
     if (!(u >= 0.0f && u < 1.0f)) st |= ST_BAD_UNIFORM;
+    bool placed = false;
     for (int s = 0; s < d.n_shards; ++s) {
       const dsv41_full_pick& pk = d.picks[(int64_t)s * d.rows + row];
       if (pk.id >= 0) {
         tok = pk.id;
         ztok = pk.z;
+        placed = true;
         break;
       }
     }
+    // a finite row always has mass (its maximum weighs 2^43), so some slice places it
+    if (!placed && !(st & ST_NONFINITE)) st |= ST_BAD_SLICES;
   }
-  if (st & ST_NONFINITE) {
+  if (st & (ST_NONFINITE | ST_BAD_SLICES)) {
     d.out_ids[row] = -1;
     d.out_logprob[row] = __builtin_nanf("");
     if (d.out_kept) d.out_kept[row] = 0;
@@ -3202,6 +3218,7 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.hlen = d->hist_len;
   p.top_k = pl.internal_k ? INTERNAL_K : d->top_k;
   p.topk_internal = pl.internal_k ? 1 : 0;
+  p.mid_trigger = pl.internal_k ? INT_MAX : 2 * d->top_k + 128;
   p.greedy = d->greedy ? 1 : 0;
   p.has_pen = pl.has_pen ? 1 : 0;
   p.pen_lowers = pl.has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&

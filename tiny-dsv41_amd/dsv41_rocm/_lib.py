@@ -30,6 +30,7 @@ STATUS_BAD_HISTORY = 2
 STATUS_BAD_UNIFORM = 4
 STATUS_RATIO_ZERO = 8
 STATUS_BAD_TARGET = 16
+STATUS_BAD_SLICES = 32
 
 
 class SamplerDesc(ctypes.Structure):

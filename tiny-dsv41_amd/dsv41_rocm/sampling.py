@@ -60,6 +60,8 @@ def _status_error(status: torch.Tensor) -> None:
         raise ValueError("uniforms must lie in [0, 1)")
     if bits & _lib.STATUS_BAD_TARGET:
         raise ValueError("target token ID is outside the model vocabulary")
+    if bits & _lib.STATUS_BAD_SLICES:
+        raise ValueError("gathered slice masses do not match the draw step's inputs")
 
 
 def _rows_in(logits, history, history_lens, temperature, top_k):
