@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
         c.dsv41_check_division.argtypes = [ctypes.c_float, ctypes.c_uint32, ctypes.c_uint32,
                                            ctypes.POINTER(ctypes.c_uint32)]
         c.dsv41_oracle_sample.restype = ctypes.c_int
+        c.dsv41_oracle_full_draw.restype = ctypes.c_int64
         _lib = c
     return _lib
 
@@ -102,6 +103,19 @@ def process_row(logits, *, temperature=1.0, history=None, history_prompt_len=0, 
     return z, int(st)
 
 
+def full_draw(z, U: int, *, history_ids=None, slice_starts=None) -> int:
+    """The full-vocabulary inverse-CDF draw of processed logits ``z`` at the 32-bit uniform
+    ``U`` (u = U / 2^32); ``history_ids``: the ids the penalties processed."""
+    z = np.ascontiguousarray(np.asarray(z, dtype=np.float32))
+    counts = None
+    if history_ids is not None:
+        counts = np.zeros(z.shape[0], np.uint32)
+        counts[np.asarray(history_ids, dtype=np.int64)] = 1
+    ss = None if slice_starts is None else np.ascontiguousarray(np.asarray(slice_starts, dtype=np.int32))
+    return int(lib().dsv41_oracle_full_draw(_ptr(z), ctypes.c_int(z.shape[0]), _ptr(counts), _ptr(ss),
+                                            ctypes.c_int(0 if ss is None else ss.size), ctypes.c_uint32(U)))
+
+
 def check_division(temperature: float, lo: int, hi: int) -> tuple[int, int]:
     first = ctypes.c_uint32(0)
     n = lib().dsv41_check_division(temperature, lo, hi, ctypes.byref(first))
@@ -114,10 +128,12 @@ def _ptr(a):
 
 def sample(logits, *, temperature=1.0, uniforms=None, history=None, history_lens=None,
            repetition_penalty=1.0, presence_penalty=0.0, frequency_penalty=0.0, top_k=0,
-           top_p=1.0, min_p=0.0, greedy=False, history_prompt_lens=None):
+           top_p=1.0, min_p=0.0, greedy=False, history_prompt_lens=None, slice_starts=None):
     """Oracle sampler over fp32 logits [rows, V] (bf16 callers widen exactly first).
     ``history_prompt_lens[r]`` leading history entries of row r are prompt ids (repetition
-    penalty only; frequency and presence count the rest).
+    penalty only; frequency and presence count the rest).  ``slice_starts`` (ascending,
+    starting at 0): the vocabulary slices of a sharded full-vocabulary draw, whose 256-id
+    mass chunks restart at each slice start; None is one slice.
 
     Returns numpy (ids int64, logprobs fp32, kept int32, status int32).
     """
@@ -127,6 +143,9 @@ def sample(logits, *, temperature=1.0, uniforms=None, history=None, history_lens
     h = None if history is None else np.ascontiguousarray(np.asarray(history, dtype=np.int64))
     hl = None if history_lens is None else np.ascontiguousarray(np.asarray(history_lens, dtype=np.int32))
     pl = None if history_prompt_lens is None else np.ascontiguousarray(np.asarray(history_prompt_lens, dtype=np.int32))
+    ss = None if slice_starts is None else np.ascontiguousarray(np.asarray(slice_starts, dtype=np.int32))
+    if ss is not None and (ss.ndim != 1 or ss.size == 0 or ss[0] != 0 or np.any(np.diff(ss) <= 0)):
+        raise ValueError("slice_starts must ascend from 0")
     ids = np.empty(rows, np.int64)
     lps = np.empty(rows, np.float32)
     kept = np.empty(rows, np.int32)
@@ -138,7 +157,7 @@ def sample(logits, *, temperature=1.0, uniforms=None, history=None, history_lens
         _ptr(hl), _ptr(pl), _ptr(u), ctypes.c_float(temperature), ctypes.c_float(repetition_penalty),
         ctypes.c_float(presence_penalty), ctypes.c_float(frequency_penalty), ctypes.c_int(top_k),
         ctypes.c_float(top_p), ctypes.c_float(min_p), ctypes.c_int(1 if greedy else 0), _ptr(ids),
-        _ptr(lps), _ptr(kept), _ptr(status))
+        _ptr(lps), _ptr(kept), _ptr(status), _ptr(ss), ctypes.c_int(0 if ss is None else ss.size))
     if rc != 0:
         raise MemoryError("oracle scratch allocation failed")
     return ids, lps, kept, status

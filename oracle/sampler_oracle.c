@@ -188,13 +188,82 @@ int dsv41_oracle_process_row(const float* x, int V, const int64_t* hist, int hle
 }
 
 /*
+ * Inverse-CDF draw over the whole row (no truncation) with 256-id chunk masses.  The row
+ * is cut into chunks of MASS_CHUNK consecutive ids; chunks restart at every slice start
+ * (starts[0..n_starts), ascending, starts[0] = 0; NULL = one slice).  An id outside the
+ * history H (the ids the penalties processed, counts[v] != 0) weighs
+ *   w_v = floor(2^43 exp32(z_v - m_c)),  m_c = max of z over the chunk's ids outside H,
+ * and the chunk weighs Q_c = floor(W_c g_c / 2^43) + sum over its ids in H of
+ * floor(2^43 exp32(z_h - zmax)), with W_c = sum w_v and g_c = floor(2^43 exp32(m_c - zmax)).
+ * The target t = (S U) >> 32 with S = sum Q_c picks the first chunk whose cumulative Q
+ * exceeds t; inside it, the id boundaries in Q units are floor(prefix(w) g_c / 2^43) +
+ * prefix(history masses), in vocabulary order, and the first boundary above what the chunk
+ * owes names the token.  Every quantity is an integer, so sums in any order agree.
+ */
+#define MASS_CHUNK 256
+static int64_t full_draw(const float* z, int V, const uint32_t* counts, const int32_t* starts, int n_starts,
+                         float zmax, uint64_t U) {
+  /* chunk list: [lo, hi) per chunk; a first pass for S, a second for the token */
+  uint64_t S = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    uint64_t t = 0, before = 0;
+    if (pass == 1) t = (uint64_t)(((u128)S * U) >> 32); /* dsv41_draw_target with U = u 2^32 */
+    for (int s = 0; s < (starts ? n_starts : 1); ++s) {
+      const int a = starts ? starts[s] : 0;
+      const int b = (starts && s + 1 < n_starts) ? starts[s + 1] : V;
+      for (int lo = a; lo < b; lo += MASS_CHUNK) {
+        const int hi = lo + MASS_CHUNK < b ? lo + MASS_CHUNK : b;
+        float mc = -INFINITY;
+        for (int v = lo; v < hi; ++v)
+          if (!(counts && counts[v]) && z[v] > mc) mc = z[v];
+        const uint64_t g = dsv41_mass(mc, zmax);
+        uint64_t W = 0, Hm = 0;
+        for (int v = lo; v < hi; ++v) {
+          if (counts && counts[v]) Hm += dsv41_mass(z[v], zmax);
+          else W += dsv41_mass(z[v], mc);
+        }
+        const uint64_t Q = (uint64_t)(((u128)W * g) >> 43) + Hm;
+        if (pass == 0) {
+          S += Q;
+          continue;
+        }
+        if (t < before + Q) {
+          const uint64_t need = t - before;
+          uint64_t cw = 0, ch = 0;
+          for (int v = lo; v < hi; ++v) {
+            if (counts && counts[v]) ch += dsv41_mass(z[v], zmax);
+            else cw += dsv41_mass(z[v], mc);
+            if (need < (uint64_t)(((u128)cw * g) >> 43) + ch) return v;
+          }
+        }
+        before += Q;
+      }
+    }
+  }
+  return -1; /* no mass: only rows without a finite maximum */
+}
+
+/* The full-vocabulary inverse-CDF draw of processed logits z[V] against the 32-bit
+ * uniform U (the draw of u = U / 2^32), for the tests' interval checks. */
+int64_t dsv41_oracle_full_draw(const float* z, int V, const uint32_t* counts, const int32_t* starts,
+                               int n_starts, uint32_t U) {
+  float zmax = z[0];
+  for (int v = 1; v < V; ++v)
+    if (z[v] > zmax) zmax = z[v];
+  return full_draw(z, V, counts, starts, n_starts, zmax, U);
+}
+
+/*
  * Kept set + draw for one row of processed logits z[V].
  * Writes *id, *lp, *kept; returns status bits (BAD_UNIFORM).
- * scratch_keys: V uint64, scratch_idx: V uint32.
+ * scratch_keys: V uint64, scratch_idx: V uint32.  counts: the history membership of
+ * dsv41_oracle_process_row (NULL: none); starts / n_starts: slice starts of the
+ * full-vocabulary draw's chunks (NULL: one slice).
  */
 int dsv41_oracle_select_row(const float* z, int V, float u, int top_k, float top_p, float min_p,
                             int greedy, uint64_t* keys, uint32_t* idxs, int64_t* out_id,
-                            float* out_lp, int32_t* out_kept) {
+                            float* out_lp, int32_t* out_kept, const uint32_t* counts,
+                            const int32_t* starts, int n_starts) {
   int status = 0;
   /* first index of the maximum */
   int am = 0;
@@ -250,6 +319,14 @@ int dsv41_oracle_select_row(const float* z, int V, float u, int top_k, float top
   int64_t tok;
   if (greedy) {
     tok = am;
+  } else if (!truncating) {
+    float uu = u;
+    if (!(uu >= 0.0f && uu < 1.0f)) {
+      status |= ST_BAD_UNIFORM;
+      uu = 0.0f;
+    }
+    tok = full_draw(z, V, counts, starts, n_starts, zmax, (uint64_t)(uu * 4294967296.0f));
+    if (tok < 0) tok = am;
   } else {
     float uu = u;
     if (!(uu >= 0.0f && uu < 1.0f)) {
@@ -283,7 +360,8 @@ int dsv41_oracle_sample(const float* logits, int rows, int V, const int64_t* his
                         const float* uniforms,
                         float T, float rp, float pres, float freq, int top_k, float top_p,
                         float min_p, int greedy, int64_t* out_ids, float* out_lp,
-                        int32_t* out_kept, int32_t* out_status) {
+                        int32_t* out_kept, int32_t* out_status, const int32_t* slice_starts,
+                        int n_slices) {
   uint32_t* counts = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)V);
   float* z = (float*)malloc(sizeof(float) * (size_t)V);
   uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
@@ -308,7 +386,7 @@ int dsv41_oracle_sample(const float* logits, int rows, int V, const int64_t* his
     }
     float u = uniforms ? uniforms[r] : 0.0f;
     st |= dsv41_oracle_select_row(z, V, u, top_k, top_p, min_p, greedy, keys, idxs, &out_ids[r],
-                                  &out_lp[r], &out_kept[r]);
+                                  &out_lp[r], &out_kept[r], counts, slice_starts, n_slices);
     out_status[r] = st;
   }
   free(counts);

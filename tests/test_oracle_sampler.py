@@ -287,3 +287,77 @@ def test_torch_multinomial_is_an_exponential_race_on_the_cpu():
     bulk = torch.empty(4, 5000).exponential_(1, generator=g1)
     rows = torch.stack([torch.empty(5000).exponential_(1, generator=g2) for _ in range(4)])
     assert torch.equal(bulk, rows) and torch.equal(g1.get_state(), g2.get_state())
+
+
+def _draw_intervals(z, **kw):
+    """For every id, how many 32-bit uniforms U draw it: the draw is a non-decreasing step
+    function of U, so a binary search finds the first U of each id."""
+    V = len(z)
+    firsts = []
+    lo = 0
+    for v in range(V + 1):
+        a, b = lo, 1 << 32  # smallest U in [a, b] whose draw is >= v (U = 2^32 stands for "none")
+        while a < b:
+            mid = (a + b) // 2
+            if oracle.full_draw(z, mid, **kw) >= v:
+                b = mid
+            else:
+                a = mid + 1
+        firsts.append(a)
+        lo = a
+    return np.diff(np.array(firsts, dtype=np.int64))
+
+
+def _softmax64(z):
+    z = np.asarray(z, dtype=np.float64)
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+@pytest.mark.parametrize("case", ["plain", "history", "slices_aligned", "slices_ragged"])
+def test_full_draw_intervals_are_the_softmax(case):
+    """The full-vocabulary inverse-CDF draw over 256-id chunk masses (each chunk's masses
+    against its own maximum, scaled exactly to the row maximum; history ids against the row
+    maximum): the share of the 2^32 uniforms that draws each id equals softmax(z) in fp64
+    within fp32 accuracy.  Chunks sit at different heights (+3, 0, -5 and a far chunk at
+    -60 that must get nothing), so a missing or wrong chunk scale shows as a factor of
+    e^3 or more; the history case puts the row maximum on a history id."""
+    g = np.random.default_rng(17)
+    z = (2.0 * g.standard_normal(900)).astype(np.float32)
+    z[:256] += 3.0
+    z[512:768] -= 5.0
+    z[768:] -= 60.0
+    kw = {}
+    if case == "history":
+        hist = g.choice(900, size=60, replace=False)
+        hist[0] = int(np.argmax(z))
+        kw["history_ids"] = hist
+    if case == "slices_aligned":
+        kw["slice_starts"] = [0, 256, 768]
+    if case == "slices_ragged":
+        kw["slice_starts"] = [0, 301, 611]
+    lengths = _draw_intervals(z, **kw)
+    assert lengths.sum() == 1 << 32 and (lengths >= 0).all()
+    p = _softmax64(z)
+    share = lengths / float(1 << 32)
+    assert np.all(np.abs(share - p) <= 2e-6 * p + 5e-10), np.max(np.abs(share - p) / (p + 1e-30))
+    assert lengths[768:].sum() == 0  # e^-60 relative to the maximum: below the 2^-43 resolution
+    if case == "slices_aligned":
+        # chunks restarting at multiples of 256 are the unsliced chunks: the same draw
+        assert np.array_equal(lengths, _draw_intervals(z))
+
+
+def test_full_draw_single_chunk_is_the_plain_inverse_cdf():
+    """A row of at most 256 ids without history is one chunk whose maximum is the row
+    maximum: its masses are floor(2^43 exp32(z - zmax)) in vocabulary order, the
+    single-level inverse CDF, for every uniform of a sweep."""
+    g = np.random.default_rng(3)
+    z = g.standard_normal(200).astype(np.float32)
+    zmax = float(z.max())
+    q = np.array([oracle.mass(float(v), zmax) for v in z], dtype=object)
+    cum = np.cumsum(q)
+    S = int(cum[-1])
+    for U in list(range(0, 1 << 32, (1 << 32) // 997)) + [(1 << 32) - 1]:
+        t = (S * U) >> 32
+        want = int(np.argmax(cum > t))
+        assert oracle.full_draw(z, U) == want

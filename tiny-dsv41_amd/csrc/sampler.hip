@@ -97,6 +97,10 @@ constexpr int DRAW_STATE = 3;       // the slice's state: max, fixed-order mass,
 constexpr int DRAW_SHARD_CDF = 4;   // inverse CDF against the gathered states
 constexpr int DRAW_SHARD_RACE = 5;  // exponential race against the gathered states
 constexpr int DRAW_SHARD_MASS = 6;  // the slice's exact fixed-point mass against the gathered maximum
+constexpr int DRAW_GREEDY = 7;      // first largest logit, no draw
+// Exact masses of the inverse-CDF draws are formed per chunk of MASS_CHUNK consecutive ids
+// of the row (or slice), against the chunk's own maximum.
+constexpr int MASS_CHUNK = 256;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -186,11 +190,13 @@ template <int G>
 __host__ __device__ inline int n_chunks(int V) {
   return (V + 64 * G - 1) / (64 * G);
 }
+__host__ __device__ inline int n_mass_chunks(int V) { return (V + MASS_CHUNK - 1) / MASS_CHUNK; }
 
 // LDS layout; must agree between the launch (host) and the kernel (device).
 // bitmap u32[words] | wrank u16[words] | cnt u16[ucap] | tok u32[ucap] |
-// penx f32[ucap] (FULL) | 256 u64 radix bins | chunks (FULL: f32 max[NC], f32 sum[NC],
-// u64 exact mass[NC]) or candidates (TOPK)
+// penx f32[ucap] (FULL) | 256 u64 radix bins | chunks (FULL: u64 exact mass[NE], f32
+// max[NE], f32 sum[NC]; NE 256-id mass chunks, NC wave spans of one or two of them) or
+// candidates (TOPK)
 // ranks = false: the membership bitmap alone (no rank, count or token tables).
 template <int MODE, int G>
 __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int cap, bool ranks = true) {
@@ -211,7 +217,7 @@ __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int ca
   l.hist256 = off;
   off += 256 * 8;
   l.mode0 = off;
-  if (MODE == MODE_FULL) off += 16 * (size_t)n_chunks<G>(V);  // max, sum (fp32), exact mass (u64)
+  if (MODE == MODE_FULL) off += 4 * (size_t)n_chunks<G>(V) + 12 * (size_t)n_mass_chunks(V);
   if (MODE == MODE_TOPK) off += 8 * (size_t)cap;
   if (MODE == MODE_TOPP) off += 8 * ((size_t)TOPP_BINS + (size_t)n_chunks<G>(V) + (size_t)cap);
   l.total = align16(off);
@@ -251,12 +257,13 @@ __device__ __forceinline__ double exp_det(double d) {
 // Fixed-point mass of a token, floor(2^43 * exp(z - zmax)), as an exact integer-valued
 // float: the same fp32 operations as the oracle's specification (d = z - zmax, 0 below -40
 // and for NaN; Cody-Waite reduction by a two-part ln 2; degree-7 Taylor polynomial in
-// Horner form with fma; exact scale by 2^(n + 43); floor).  The range checks are a clamp
-// and one select here; every step is exact or correctly rounded, so the integer is the
-// oracle's bit for bit.  The result has at most 24 significant bits and is at most 2^43.
+// Horner form with fma; exact scale by 2^(n + 43); floor).  The range checks are one clamp
+// here: fmaxf takes -40 for NaN, and d = -40 itself yields floor(2^43 e^-40 (1 + eps)) = 0,
+// so every d the oracle maps to 0 gives 0.  Every step is exact or correctly rounded, so
+// the integer is the oracle's bit for bit.  The result has at most 24 significant bits and
+// is at most 2^43.
 __device__ __forceinline__ float mass_ff(float z, float zmax) {
   float d = z - zmax;
-  const bool ok = d >= -40.0f;  // false for NaN
   d = fminf(fmaxf(d, -40.0f), 0.0f);
   const float n = __builtin_rintf(d * 0x1.715476p+0f);
   float r = __builtin_fmaf(-n, 0x1.62e4p-1f, d);
@@ -269,8 +276,7 @@ __device__ __forceinline__ float mass_ff(float z, float zmax) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  const float f = __builtin_floorf(__builtin_ldexpf(p, (int)n + 43));
-  return ok ? f : 0.0f;
+  return __builtin_floorf(__builtin_ldexpf(p, (int)n + 43));
 }
 
 __device__ __forceinline__ uint64_t mass_of(float z, float zmax) { return (uint64_t)mass_ff(z, zmax); }
@@ -919,11 +925,42 @@ __device__ __forceinline__ Hist hist_tables(unsigned char* smem, const Layout& L
   return h;
 }
 
+// Row (16-lane) maxima of v, the same value in every lane: r[k] over lanes 16k .. 16k+15.
+__device__ __forceinline__ void row_max4(float v, float (&r)[4]) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
+  r[0] = rl(v, 0);
+  r[1] = rl(v, 16);
+  r[2] = rl(v, 32);
+  r[3] = rl(v, 48);
+}
+// Each lane's 16-lane row total of v (fp64, by the same DPP steps).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double row_sum_f64(double v) {
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x124>(v);
+  v += dpp_f64<0x128>(v);
+  return v;
+}
+// floor(w * g / 2^43) for w < 2^52 and an integer-valued g <= 2^43 (a mass_ff result).
+__device__ __forceinline__ uint64_t scale_mass(uint64_t w, float g) {
+  return (uint64_t)(((unsigned __int128)w * (uint64_t)g) >> 43);
+}
+
 // ====================================================================== FULL
 // No truncation: kept set = whole vocabulary.  Chunk c = [c*64G, (c+1)*64G) is one
 // wave's span of one tile; its (max, sum exp(z - max)) go to LDS.
 template <typename TIn, int G, bool VEC, int DRAW>
-__global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
+__global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
   const Layout L = make_layout<MODE_FULL, G>(p.V, p.words, p.ucap, 0);
@@ -931,8 +968,22 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   const Hist h = hist_tables(smem, L);
   float* penz = reinterpret_cast<float*>(smem + L.penx);
   const int NC = n_chunks<G>(p.V);
-  float* cm = reinterpret_cast<float*>(smem + L.mode0);
-  float* cs = cm + NC;
+  const int NE = n_mass_chunks(p.V);
+  uint64_t* cq = reinterpret_cast<uint64_t*>(smem + L.mode0);  // exact masses of the 256-id chunks
+  float* em = reinterpret_cast<float*>(cq + NE);  // 256-id chunk maxima over ids outside the history
+  float* cs = em + NE;                            // wave-span sums of exp(z - span maximum)
+  // the maximum of wave span c: one 256-id chunk (G = 4) or two (G = 8)
+  auto span_max = [&](int c) {
+    if (G == 4) return em[c];
+    return 2 * c + 1 < NE ? fmaxf(em[2 * c], em[2 * c + 1]) : em[2 * c];
+  };
+  constexpr bool SLICE = DRAW == DRAW_STATE || DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_RACE ||
+                         DRAW == DRAW_SHARD_MASS;
+  // Inverse-CDF draws take exact fixed-point masses (see below) in the same pass as the
+  // maximum: w_i = floor(2^43 exp32(z_i - m_c)) against the maximum m_c of the token's
+  // 256-id chunk, summed exactly per chunk.
+  constexpr bool EXACT = DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_MASS;
+  static_assert(64 * G == MASS_CHUNK || 64 * G == 2 * MASS_CHUNK, "a wave span holds one or two mass chunks");
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   HistIds<HR> hi;
@@ -946,8 +997,10 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
+        if constexpr (EXACT)
+          for (int e = tid; e < NE; e += NT) cq[e] = 0;
         __syncthreads();
-        if (p.has_pen) U = build_history<NT, HR, (DRAW >= DRAW_STATE)>(p, row, hi, h, m);
+        if (p.has_pen) U = build_history<NT, HR, SLICE>(p, row, hi, h, m);
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
@@ -964,7 +1017,25 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
             float mx = z[0];
 #pragma unroll
             for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
-            mx = wave_max_dpp(mx);
+            float rmx[4];
+            row_max4(mx, rmx);
+            mx = fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
+            // the lane's 256-id chunk (a wave span holds one chunk, or two: lanes 0-31 and
+            // 32-63) and its maximum
+            const float mc = G == 4 ? mx : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
+            const int e = (t * TILE + wid * 64 * G) / MASS_CHUNK + (G == 4 ? 0 : (lane >> 5));
+            if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) em[e] = mc;
+            if constexpr (EXACT) {
+              // the lane's masses against its chunk's maximum: integers of at most 2^43, so
+              // the fp64 sums below are exact in any order (a chunk's total is below 2^51)
+              double qd = 0.0;
+#pragma unroll
+              for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
+              const double rs4 = row_sum_f64(qd);  // the lane's 16-lane row total
+              // rows 0 + 1 (and 2 + 3) are one chunk: each row's lane 0 adds its total
+              if ((lane & 15) == 0 && e < NE)
+                atomicAdd(reinterpret_cast<unsigned long long*>(&cq[e]), (unsigned long long)rs4);
+            }
             float s = 0.0f;
             if (mx > NEG_INF) {
               const float mb = mx * LOG2E;
@@ -973,10 +1044,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
             }
             s = wave_sum_dpp(s);
             const int c = t * NW + wid;
-            if (lane == 0 && c < NC) {
-              cm[c] = mx;
-              cs[c] = s;
-            }
+            if (lane == 0 && c < NC) cs[c] = s;
           }
         }
         for (int i = tid; i < n; i += NT) {
@@ -993,13 +1061,20 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   float pmax = NEG_INF;
   for (int s = tid; s < U; s += NT) pmax = fmaxf(pmax, penz[s]);
   float cmax = NEG_INF;
-  for (int c = tid; c < NC; c += NT) cmax = fmaxf(cmax, cm[c]);
+  for (int c = tid; c < NE; c += NT) cmax = fmaxf(cmax, em[c]);
   const float M = block_max<NT>(fmaxf(pmax, cmax), m);
 
-  // rescale chunk sums to the row maximum, then add the history tokens
-  for (int c = tid; c < NC; c += NT) cs[c] = cm[c] > NEG_INF ? cs[c] * exp2f((cm[c] - M) * LOG2E) : 0.0f;
-  __syncthreads();
-  for (int s = tid; s < U; s += NT) atomicAdd(&cs[h.tok[s] / (64 * G)], exp2f((penz[s] - M) * LOG2E));
+  // rescale chunk sums to the row maximum and add the chunk's history tokens: their slots
+  // are in id order, so a chunk's slots are one run, summed in order by one thread
+  for (int c = tid; c < NC; c += NT) {
+    const float sm = span_max(c);
+    float v = sm > NEG_INF ? cs[c] * exp2f((sm - M) * LOG2E) : 0.0f;
+    if (p.has_pen) {
+      const int s1 = rank_below(h, min((c + 1) * 64 * G, p.V), p.words, U);
+      for (int s = rank_below(h, c * 64 * G, p.words, U); s < s1; ++s) v += exp2f((penz[s] - M) * LOG2E);
+    }
+    cs[c] = v;
+  }
   __syncthreads();
 
   // Row total over the chunk table in one fixed order (lane l of wave 0 sums a contiguous
@@ -1143,17 +1218,19 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     return;
   }
 
-  // Inverse-CDF draws use 2^-43 fixed-point masses q_i = floor(2^43 exp(z_i - Mref))
-  // against the row's maximum Mref (a slice: the maximum over all slices), as the oracle and
-  // the truncating kernels do.  Integer sums are associative, so the drawn id does not depend
-  // on the order of any reduction.  A second pass over the row sums each chunk's masses into
-  // cq; the token's place inside its chunk comes from the masses of one more read of that
-  // chunk.  The log-prob keeps the fp32 chunk total above, which every full-vocabulary draw
-  // and the replay share.
+  // Inverse-CDF draws use 2^-43 fixed-point masses, exact integers, so the drawn id does
+  // not depend on the order of any reduction.  The row (or slice) is cut into 256-id
+  // chunks.  In the stream, an id outside the history got w_i = floor(2^43 exp32(z_i - m_c))
+  // against its chunk's maximum m_c over such ids, and cq[c] = W_c = sum w_i.  With the row's
+  // maximum Mref known (a slice: the maximum over all slices), the chunk weighs
+  //   Q_c = floor(W_c g_c / 2^43),  g_c = floor(2^43 exp32(m_c - Mref)),
+  // plus the history ids' masses floor(2^43 exp32(z_h - Mref)); the oracle defines the same
+  // integers.  Inside the chunk holding the target, the id boundaries in Q units are
+  // floor(prefix(w) g_c / 2^43) + prefix(history masses), in vocabulary order.  The
+  // log-prob keeps the fp32 chunk total above, which every full-vocabulary draw and the
+  // replay share.
   constexpr bool SHARDED = DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_MASS;
-  const bool exact = SHARDED || (DRAW == DRAW_CDF && !p.greedy);
   const float u = (DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF) ? row_uniform(p, row, m) : 0.0f;
-  uint64_t* cq = reinterpret_cast<uint64_t*>(smem + L.mode0 + 8 * (size_t)NC);
   float Mref = M;
   uint64_t tq = 0;  // the draw's target in this workgroup's masses
   if constexpr (SHARDED) {
@@ -1181,38 +1258,22 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       return;
     }
   }
-  if (exact) {
-    const int nt = (p.V + TILE - 1) / TILE;
-    Raw<TIn, G> R0, R1;
-    load_group<TIn, G, VEC, FULL_CPOL>(R0, rs, tid * G);
-    for (int t = 0; t < nt; ++t) {
-      load_group<TIn, G, VEC, FULL_CPOL>(R1, rs, (t + 1) * TILE + tid * G);  // past the row: zeros
-      const int base = t * TILE + tid * G;
-      float x[G], z[G];
-      unpack(R0, x);
-      int dummy = 0;
-      make_z<G, true>(x, base, p, h.bitmap, z, dummy);  // history tokens and the tail read -inf
-      // the G masses are integers of at most 2^43: their sum is exact in fp64
-      double qd = 0.0;
-#pragma unroll
-      for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], Mref);
-      uint64_t q = (uint64_t)qd;
-      q = wave_sum_u64(q);
-      const int c = t * NW + wid;
-      if (lane == 0 && c < NC) cq[c] = q;
-      R0 = R1;
+  if constexpr (EXACT) {
+    for (int c = tid; c < NE; c += NT) {
+      uint64_t q = scale_mass(cq[c], mass_ff(em[c], Mref));
+      if (p.has_pen) {
+        const int s1 = rank_below(h, min((c + 1) * MASS_CHUNK, p.V), p.words, U);
+        for (int s = rank_below(h, c * MASS_CHUNK, p.words, U); s < s1; ++s) q += mass_of(penz[s], Mref);
+      }
+      cq[c] = q;
     }
-    __syncthreads();
-    for (int s = tid; s < U; s += NT)
-      atomicAdd(reinterpret_cast<unsigned long long*>(&cq[h.tok[s] / (64 * G)]),
-                (unsigned long long)mass_of(penz[s], Mref));
     __syncthreads();
   }
   if constexpr (DRAW == DRAW_SHARD_MASS) {
     // this slice's exact mass against the gathered maximum; the draw step gathers them
     if (wid == 0) {
       uint64_t s = 0;
-      for (int c = lane; c < NC; c += 64) s += cq[c];
+      for (int c = lane; c < NE; c += 64) s += cq[c];
       s = wave_sum_u64(s);
       if (lane == 0) p.sh_out_masses[row] = s;
     }
@@ -1221,10 +1282,10 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
   if (wid == 0) {
     double own, incl;
     const double S = chunk_total(incl, own);  // the log-prob's total
-    if (exact) {
+    if constexpr (EXACT) {
       // the chunk holding the target: lane l sums a contiguous run of chunks, then a scan
-      const int per = (NC + 63) / 64;
-      const int b = lane * per, e = min(b + per, NC);
+      const int per = (NE + 63) / 64;
+      const int b = lane * per, e = min(b + per, NE);
       uint64_t s = 0;
       for (int c = b; c < e; ++c) s += cq[c];
       const uint64_t qincl = wave_incl_scan_u64(s, lane);
@@ -1255,15 +1316,17 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
     }
     if (lane == 0) m->bd[1] = S;
   }
-  // first chunk whose maximum is the row maximum, first history token at it (greedy)
-  int cfirst = NC;
-  for (int c = tid; c < NC; c += NT)
-    if (cm[c] == M) cfirst = min(cfirst, c);
-  int pfirst = 0x7FFFFFFF;
-  for (int s = tid; s < U; s += NT)
-    if (penz[s] == M) pfirst = min(pfirst, (int)h.tok[s]);
-  cfirst = block_min_i<NT>(cfirst, m);
-  pfirst = block_min_i<NT>(pfirst, m);
+  // first chunk whose maximum is the row maximum, first history token at it (greedy; a
+  // uniform condition, so the block reductions inside are reached by every thread or none)
+  int cfirst = NC, pfirst = 0x7FFFFFFF;
+  if (!EXACT || p.greedy) {
+    for (int c = tid; c < NC; c += NT)
+      if (span_max(c) == M) cfirst = min(cfirst, c);
+    for (int s = tid; s < U; s += NT)
+      if (penz[s] == M) pfirst = min(pfirst, (int)h.tok[s]);
+    cfirst = block_min_i<NT>(cfirst, m);
+    pfirst = block_min_i<NT>(pfirst, m);
+  }
 
   if (wid == 0) {
     const double S = m->bd[1];
@@ -1286,7 +1349,7 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
         }
       }
     };
-    if (p.greedy || DRAW == DRAW_STATE) {  // the state carries the first argmax
+    if (!EXACT || p.greedy) {  // greedy; the state carries the first argmax
       int best = pfirst;
       if (cfirst < NC) {
         float z[G];
@@ -1301,30 +1364,48 @@ __global__ __launch_bounds__(FULL_NT) void full_kernel(Params p) {
       }
       tok = best;
       ztok = M;
-    } else if (m->bi[0] >= 0) {
-      // the first token of the chunk whose cumulative mass exceeds what the chunk owes
-      const int cstar = m->bi[0];
+    } else if (EXACT && m->bi[0] >= 0) {
+      // The first id of the target's chunk whose boundary in Q units exceeds what the chunk
+      // owes: lanes 0 .. 256/G - 1 hold the chunk's 256 ids.  An id outside the history
+      // carries w_i against the chunk maximum, a history id its mass against Mref.
+      const int ce = m->bi[0];
       const uint64_t need = m->bu[0];
-      const int base = cstar * 64 * G + lane * G;
-      float z[G];
-      chunk_z(cstar, z);
-      uint64_t q[G];
-      uint64_t ls = 0;
+      const float mc = em[ce];
+      const float g = mass_ff(mc, Mref);
+      const bool act = lane < MASS_CHUNK / G;
+      const int base = ce * MASS_CHUNK + lane * G;
+      Raw<TIn, G> r;
+      load_group<TIn, G, VEC, FULL_CPOL>(r, rs, base);  // lanes past the chunk: not used
+      float x[G], z[G];
+      unpack(r, x);
+      int dummy = 0;
+      make_z<G, true>(x, base, p, h.bitmap, z, dummy);  // history ids and the tail read -inf
+      uint64_t wq[G], hq[G];
+      uint64_t sw = 0, sh = 0;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        q[j] = mass_of(z[j], Mref);
-        ls += q[j];
+        const int v = base + j;
+        const bool hist = act && p.has_pen && v < p.V && ((h.bitmap[v >> 5] >> (v & 31)) & 1u);
+        wq[j] = act ? mass_of(z[j], mc) : 0;
+        hq[j] = 0;
+        if (hist) {
+          z[j] = penz[slot_of(h, v)];
+          hq[j] = mass_of(z[j], Mref);
+        }
+        sw += wq[j];
+        sh += hq[j];
       }
-      uint64_t acc = wave_incl_scan_u64(ls, lane) - ls;
+      uint64_t cw = wave_incl_scan_u64(sw, lane) - sw, ch = wave_incl_scan_u64(sh, lane) - sh;
       int pick = -1;
       float zp = NEG_INF;
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        if (pick < 0 && need < acc + q[j]) {
+        cw += wq[j];
+        ch += hq[j];
+        if (act && pick < 0 && need < scale_mass(cw, g) + ch) {
           pick = base + j;
           zp = z[j];
         }
-        acc += q[j];
       }
       const unsigned long long hit = __ballot(pick >= 0);
       if (hit) {
@@ -3328,6 +3409,12 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
                               : launch(full_kernel<uint16_t, 8, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
         return pl.vec ? launch(full_kernel<float, 4, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
                       : launch(full_kernel<float, 4, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
+      }
+      if (p.greedy) {
+        if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s)
+                              : launch(full_kernel<uint16_t, 8, false, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 4, false, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s);
       }
       if (p.exps) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s)
