@@ -158,3 +158,30 @@ def test_decode_loop_finish_reasons_and_errors():
         generate_response(model, [0], 3, 0.0)
     with pytest.raises(ValueError, match="CPU torch.Generator"):
         generate_response(model, [0], 3, 1.0, generator=torch.Generator(device=DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sample_next_step_equals_sample(dtype):
+    """sample_next's batch-1 inverse-CDF step (buffers kept across calls, uniform and outputs
+    through a pinned host block, one synchronisation) returns what sample() returns for the
+    same row and the same uniform, bit for bit, and leaves the generator where sample()'s
+    torch.rand leaves it; a non-finite row raises the reference's message."""
+    from dsv41_rocm import sample, sample_next
+    g = torch.Generator().manual_seed(99)
+    rows = (2.5 * torch.randn(12, 151936, generator=g)).to(dtype).to(DEV)
+    ga, gb = torch.Generator().manual_seed(5), torch.Generator().manual_seed(5)
+    for i in range(rows.shape[0]):
+        T = (0.6, 1.0, 1.3)[i % 3]
+        print(f"case: sample_next step {i} dtype={dtype} T={T}", flush=True)
+        tok, lp = sample_next(rows[i], T, generator=ga)
+        u = torch.rand(1, generator=gb)
+        ref = sample(rows[i:i + 1], temperature=T, uniforms=u.to(DEV))
+        assert tok == int(ref.ids[0])
+        assert torch.tensor([lp], dtype=torch.float32).view(torch.int32) == ref.logprobs.cpu().view(torch.int32)
+    assert torch.equal(ga.get_state(), gb.get_state())
+    bad = rows[0].clone()
+    bad[7] = float("nan")
+    with pytest.raises(ValueError, match="generation log probabilities contain non-finite values"):
+        sample_next(bad, 1.0, generator=ga)
+    with pytest.raises(ValueError, match="temperature must be finite and positive"):
+        sample_next(rows[0], 0.0, generator=ga)

@@ -632,3 +632,38 @@ def test_largest_vocabulary(V, dtype, knobs):
     gpu, ora = run_both(x.to(dtype), None if knobs.get("greedy") else u, hist, temperature=0.8, **knobs)
     assert_exact(gpu, ora)
     assert (ora[3] == 0).all()
+
+
+@pytest.mark.parametrize("rows,V,dtype", [(1, 151936, torch.float32), (3, 151936, torch.bfloat16),
+                                          (8, 129280, torch.float32), (100, 5003, torch.float32),
+                                          (128, 1000, torch.bfloat16)])
+@pytest.mark.parametrize("greedy", [False, True])
+def test_small_full_batches_spread_over_the_gpu(rows, V, dtype, greedy):
+    """Full-vocabulary batches of at most 128 rows without penalties are spread over the GPU
+    (slices of wave spans, then one finishing workgroup per row).  Their ids and log-probs
+    equal, bit for bit, those of the same rows drawn inside a 200-row batch (one workgroup
+    per row, the stream of the same kernel), and the oracle's; the replay of every drawn
+    token returns the drawn log-prob bit for bit."""
+    from dsv41_rocm import replay_log_probs
+    g = torch.Generator().manual_seed(rows * 7 + V)
+    x = (2.0 * torch.randn(200, V, generator=g)).to(dtype)
+    u = torch.rand(200, generator=g)
+    x[min(2, rows - 1) if rows > 1 else 150, V // 3] = float("nan")  # a non-finite row
+    u[min(1, rows - 1) if rows > 1 else 151] = 1.25  # a bad uniform
+    knobs = dict(temperature=0.7, greedy=greedy)
+    xd, ud = x.to(DEV), u.to(DEV)
+    print(f"case: spread FULL batch rows={rows} V={V} dtype={dtype} greedy={greedy}", flush=True)
+    small = sample(xd[:rows], uniforms=None if greedy else ud[:rows], check=False, **knobs)
+    whole = sample(xd, uniforms=None if greedy else ud, check=False, **knobs)
+    torch.cuda.synchronize()
+    for name in ("ids", "kept", "status"):
+        assert torch.equal(getattr(small, name), getattr(whole, name)[:rows]), name
+    ok = small.status == 0
+    assert torch.equal(small.logprobs[ok].view(torch.int32), whole.logprobs[:rows][ok].view(torch.int32))
+    ora = oracle.sample(x[:rows].float().numpy(), uniforms=None if greedy else u[:rows].numpy(),
+                        temperature=0.7, greedy=greedy)
+    assert_exact(tuple(t.cpu().numpy() for t in (small.ids, small.logprobs, small.kept, small.status)), ora)
+    if bool(ok.any()):
+        okr = ok.nonzero().flatten()
+        rep = replay_log_probs(xd[:rows][okr], small.ids[okr], temperature=0.7)
+        assert torch.equal(rep.view(torch.int32), small.logprobs[okr].view(torch.int32))

@@ -101,6 +101,8 @@ constexpr int DRAW_GREEDY = 7;      // first largest logit, no draw
 // Exact masses of the inverse-CDF draws are formed per chunk of MASS_CHUNK consecutive ids
 // of the row (or slice), against the chunk's own maximum.
 constexpr int MASS_CHUNK = 256;
+// FULL batches of at most this many rows without penalties are spread over the GPU
+constexpr int PRE_MAX_ROWS = 128;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -158,6 +160,13 @@ struct Params {
   // TOPK with lowering penalties and no frequency penalty needs only the membership
   // bitmap: ucap is 0 then and the rank table is left out of the layout
   int no_ranks;
+  // small FULL batch spread over the GPU: full_slice_kernel writes each row's wave-span
+  // sums [rows, NC], 256-id chunk maxima and exact masses [rows, NE] and per-slice status
+  // [rows, n_slices] (slice_w wave spans per slice); full_kernel<..., PRE> finishes rows
+  float* pre_cs;
+  float* pre_em;
+  uint64_t* pre_w;
+  int32_t* pre_st;
 };
 
 // Per-workgroup scalars and reduction scratch, at the start of dynamic LDS.
@@ -956,10 +965,99 @@ __device__ __forceinline__ uint64_t scale_mass(uint64_t w, float g) {
   return (uint64_t)(((unsigned __int128)w * (uint64_t)g) >> 43);
 }
 
+// Statistics of one wave span of 64 G processed logits (lane l holds z for ids l G ..
+// l G + G - 1 of the span): mx = the span maximum; mc = the maximum of the lane's 256-id mass
+// chunk (the span, or its half: lanes 0-31 and 32-63); s = the wave sum of exp(z - mx) in
+// fp32, the same in every lane; (EXACT) rs4 = the lane's 16-lane row total of the masses
+// floor(2^43 exp32(z - mc)), integers of at most 2^43, so the fp64 sums are exact in any
+// order (a chunk's total is below 2^51).
+template <int G, bool EXACT>
+__device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float& mx, float& mc, float& s,
+                                           double& rs4) {
+  mx = z[0];
+#pragma unroll
+  for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
+  float rmx[4];
+  row_max4(mx, rmx);
+  mx = fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
+  mc = G == 4 ? mx : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
+  if constexpr (EXACT) {
+    double qd = 0.0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
+    rs4 = row_sum_f64(qd);
+  }
+  s = 0.0f;
+  if (mx > NEG_INF) {
+    const float mb = mx * LOG2E;
+#pragma unroll
+    for (int j = 0; j < G; ++j) s += exp2f(__builtin_fmaf(z[j], LOG2E, -mb));
+  }
+  s = wave_sum_dpp(s);
+}
+
+__device__ __forceinline__ double rl_d(double v, int lane) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// A small batch without penalties spread over the GPU: workgroup b takes slice b % n_slices
+// (slice_w wave spans of 64 G ids) of row b / n_slices, one span per wave at a time, and
+// writes the span statistics full_kernel's stream forms (span_stats on the same z), so
+// full_kernel<..., PRE> finishes each row with the values and the order of the one-workgroup
+// kernel: the same ids and log-probs, bit for bit.
+constexpr int PRE_NT = 256;
+template <typename TIn, int G, bool VEC, bool EXACT>
+__global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
+  constexpr int NW = PRE_NT / 64;
+  const int row = blockIdx.x / p.n_slices, sl = blockIdx.x % p.n_slices;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int NC = n_chunks<G>(p.V), NE = n_mass_chunks(p.V);
+  const int c1 = min((sl + 1) * p.slice_w, NC);
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(row_ptr<TIn>(p, row), (uint32_t)p.V * (uint32_t)sizeof(TIn));
+  float* ocs = p.pre_cs + (int64_t)row * NC;
+  float* oem = p.pre_em + (int64_t)row * NE;
+  uint64_t* ow = p.pre_w + (int64_t)row * NE;
+  int bad = 0;
+  int c = sl * p.slice_w + wid;
+  Raw<TIn, G> A;
+  if (c < c1) load_group<TIn, G, VEC, FULL_CPOL>(A, rs, c * 64 * G + lane * G);
+  while (c < c1) {  // uniform per wave; the next span's load is in flight meanwhile
+    const int cn = c + NW;
+    Raw<TIn, G> B;
+    if (cn < c1) load_group<TIn, G, VEC, FULL_CPOL>(B, rs, cn * 64 * G + lane * G);
+    const int base = c * 64 * G + lane * G;
+    float x[G], z[G];
+    unpack(A, x);
+    make_z<G, true>(x, base, p, nullptr, z, bad);  // no penalties here; ids past V read -inf
+    float mx, mc, s;
+    double rs4 = 0.0;
+    span_stats<G, EXACT>(z, lane, mx, mc, s, rs4);
+    if (lane == 0) ocs[c] = s;
+    const int e = c * (64 * G / MASS_CHUNK) + (G == 4 ? 0 : (lane >> 5));
+    if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) oem[e] = mc;
+    if constexpr (EXACT) {
+      const double r0 = rl_d(rs4, 0), r1 = rl_d(rs4, 16), r2 = rl_d(rs4, 32), r3 = rl_d(rs4, 48);
+      if (G == 4) {
+        if (lane == 0 && e < NE) ow[e] = (uint64_t)((r0 + r1) + (r2 + r3));
+      } else {
+        if (lane == 0 && e < NE) ow[e] = (uint64_t)(r0 + r1);
+        if (lane == 32 && e < NE) ow[e] = (uint64_t)(r2 + r3);
+      }
+    }
+    if (cn < c1) A = B;
+    c = cn;
+  }
+  bad = __syncthreads_or(bad);
+  if (tid == 0) p.pre_st[(int64_t)row * p.n_slices + sl] = bad ? ST_NONFINITE : 0;
+}
+
 // ====================================================================== FULL
 // No truncation: kept set = whole vocabulary.  Chunk c = [c*64G, (c+1)*64G) is one
 // wave's span of one tile; its (max, sum exp(z - max)) go to LDS.
-template <typename TIn, int G, bool VEC, int DRAW>
+template <typename TIn, int G, bool VEC, int DRAW, bool PRE = false>
 __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -986,13 +1084,27 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   static_assert(64 * G == MASS_CHUNK || 64 * G == 2 * MASS_CHUNK, "a wave span holds one or two mass chunks");
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  HistIds<HR> hi;
-  load_history<NT, HR>(p, row, hi);
   const TIn* src = row_ptr<TIn>(p, row);
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
   constexpr int TILE = NT * G;
   int bad = 0;
   int U = 0;
+  if constexpr (PRE) {
+    // the span statistics full_slice_kernel formed (no penalties on this path)
+    if (tid == 0) m->status = 0;
+    const float* pcs = p.pre_cs + (int64_t)row * NC;
+    const float* pem = p.pre_em + (int64_t)row * NE;
+    const uint64_t* pw = p.pre_w + (int64_t)row * NE;
+    for (int c = tid; c < NC; c += NT) cs[c] = pcs[c];
+    for (int e = tid; e < NE; e += NT) {
+      em[e] = pem[e];
+      if constexpr (EXACT) cq[e] = pw[e];
+    }
+    for (int s = tid; s < p.n_slices; s += NT) bad |= p.pre_st[(int64_t)row * p.n_slices + s];
+    __syncthreads();  // status cleared before any thread sets a bit
+  } else {
+  HistIds<HR> hi;
+  load_history<NT, HR>(p, row, hi);
   stream_row<TIn, G, NT, VEC, false, FULL_CPOL>(
       p, rs, h,
       [&]() {
@@ -1014,35 +1126,16 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
             unpack(R[k], x);
             if ((t + 1) * TILE <= p.V) make_z<G, false>(x, base, p, h.bitmap, z, bad);
             else make_z<G, true>(x, base, p, h.bitmap, z, bad);
-            float mx = z[0];
-#pragma unroll
-            for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
-            float rmx[4];
-            row_max4(mx, rmx);
-            mx = fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
-            // the lane's 256-id chunk (a wave span holds one chunk, or two: lanes 0-31 and
-            // 32-63) and its maximum
-            const float mc = G == 4 ? mx : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
+            float mx, mc, s;
+            double rs4 = 0.0;
+            span_stats<G, EXACT>(z, lane, mx, mc, s, rs4);
+            // the lane's 256-id chunk: the span, or its half for G = 8
             const int e = (t * TILE + wid * 64 * G) / MASS_CHUNK + (G == 4 ? 0 : (lane >> 5));
             if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) em[e] = mc;
-            if constexpr (EXACT) {
-              // the lane's masses against its chunk's maximum: integers of at most 2^43, so
-              // the fp64 sums below are exact in any order (a chunk's total is below 2^51)
-              double qd = 0.0;
-#pragma unroll
-              for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
-              const double rs4 = row_sum_f64(qd);  // the lane's 16-lane row total
-              // rows 0 + 1 (and 2 + 3) are one chunk: each row's lane 0 adds its total
+            // rows 0 + 1 (and 2 + 3) are one chunk: each row's lane 0 adds its total
+            if constexpr (EXACT)
               if ((lane & 15) == 0 && e < NE)
                 atomicAdd(reinterpret_cast<unsigned long long*>(&cq[e]), (unsigned long long)rs4);
-            }
-            float s = 0.0f;
-            if (mx > NEG_INF) {
-              const float mb = mx * LOG2E;
-#pragma unroll
-              for (int j = 0; j < G; ++j) s += exp2f(__builtin_fmaf(z[j], LOG2E, -mb));
-            }
-            s = wave_sum_dpp(s);
             const int c = t * NW + wid;
             if (lane == 0 && c < NC) cs[c] = s;
           }
@@ -1055,6 +1148,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
           penz[s] = z;
         }
       });
+  }
   if (bad) atomicOr(&m->status, ST_NONFINITE);
   __syncthreads();
 
@@ -3112,6 +3206,10 @@ struct Plan {
   // LDS, and the workspace offsets of the slices' keys, counts and statuses
   int slices, slice_w, slice_words, slice_ucap;
   size_t slice_lds, merge_lds, ws_counts, ws_status;
+  // small FULL batch without penalties over pre_slices slices of pre_sw wave spans per row
+  // (full_slice_kernel + full_kernel<..., PRE>), with the workspace offsets of its arrays
+  int pre_slices, pre_sw;
+  size_t pre_cs, pre_em, pre_w, pre_st;
 };
 
 // shard: the descriptor describes one vocabulary slice (dsv41_sampler_shard_run); the draw
@@ -3251,6 +3349,31 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
       }
     }
   }
+  // A FULL batch of at most PRE_MAX_ROWS rows without penalties leaves most CUs idle with one
+  // workgroup per row: about 512 workgroups then each take a run of a row's wave spans
+  // (full_slice_kernel), and one workgroup per row finishes it from their statistics.
+  pl->pre_slices = 0;
+  if (!shard && pl->mode == MODE_FULL && !pl->has_pen && !d->replay_ids && !d->exponentials &&
+      d->rows <= PRE_MAX_ROWS) {
+    const int G = pl->esize == 4 ? 4 : 8;
+    const int NC = (V + 64 * G - 1) / (64 * G), NE = n_mass_chunks(V);
+    const int want = std::max(2, 512 / d->rows);
+    const int sw = std::max(PRE_NT / 64, (NC + want - 1) / want);  // at least one span per wave
+    const int S = (NC + sw - 1) / sw;
+    if (S >= 2) {
+      pl->pre_slices = S;
+      pl->pre_sw = sw;
+      size_t off = align16(pl->workspace);
+      pl->pre_cs = off;
+      off = align16(off + (size_t)d->rows * NC * sizeof(float));
+      pl->pre_em = off;
+      off = align16(off + (size_t)d->rows * NE * sizeof(float));
+      pl->pre_w = off;
+      off = align16(off + (size_t)d->rows * NE * sizeof(uint64_t));
+      pl->pre_st = off;
+      pl->workspace = off + (size_t)d->rows * S * sizeof(int32_t);
+    }
+  }
   if (pl->mode == MODE_GENERIC || pl->mode == MODE_TOPP || pl->internal_k) {
     pl->workspace = align16(pl->workspace);  // the z rows follow the hand-over area
     pl->workspace += (size_t)d->rows * (size_t)V * sizeof(float);
@@ -3322,6 +3445,15 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   }
   p.voff = 0;
   p.vfull = d->vocab;
+  if (pl.pre_slices) {
+    char* ws = static_cast<char*>(workspace);
+    p.n_slices = pl.pre_slices;
+    p.slice_w = pl.pre_sw;
+    p.pre_cs = reinterpret_cast<float*>(ws + pl.pre_cs);
+    p.pre_em = reinterpret_cast<float*>(ws + pl.pre_em);
+    p.pre_w = reinterpret_cast<uint64_t*>(ws + pl.pre_w);
+    p.pre_st = reinterpret_cast<int32_t*>(ws + pl.pre_st);
+  }
   return p;
 }
 
@@ -3396,6 +3528,41 @@ static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params
                 : launch(generic_kernel<float, 4, false>, GEN_NT, lds, d->rows, g, s);
 }
 
+// A small FULL batch: the slices' statistics, then one finishing workgroup per row.
+static int run_presliced(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, hipStream_t s) {
+  const dim3 grid(d->rows * pl.pre_slices), block(PRE_NT);
+  const bool bf = pl.esize == 2, ex = !p.greedy;
+  // no dynamic LDS (a little static LDS for the block vote): no attribute to raise
+  if (bf) {
+    if (pl.vec) {
+      if (ex) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, false>), grid, block, 0, s, p);
+    } else {
+      if (ex) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, false>), grid, block, 0, s, p);
+    }
+  } else {
+    if (pl.vec) {
+      if (ex) hipLaunchKernelGGL((full_slice_kernel<float, 4, true, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<float, 4, true, false>), grid, block, 0, s, p);
+    } else {
+      if (ex) hipLaunchKernelGGL((full_slice_kernel<float, 4, false, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false, false>), grid, block, 0, s, p);
+    }
+  }
+  DSV41_HIP_CHECK(hipGetLastError());
+  if (bf) {
+    if (ex) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s)
+                          : launch(full_kernel<uint16_t, 8, false, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s);
+    return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s)
+                  : launch(full_kernel<uint16_t, 8, false, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s);
+  }
+  if (ex) return pl.vec ? launch(full_kernel<float, 4, true, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s)
+                        : launch(full_kernel<float, 4, false, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s);
+  return pl.vec ? launch(full_kernel<float, 4, true, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s)
+                : launch(full_kernel<float, 4, false, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s);
+}
+
 // The launches of one planned batch; `workspace` holds at least pl.workspace bytes.
 static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* workspace, void* stream) {
   int rc;
@@ -3404,6 +3571,7 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
   const bool bf = pl.esize == 2;
   switch (pl.mode) {
     case MODE_FULL:
+      if (pl.pre_slices) return run_presliced(d, pl, p, s);
       if (p.replay) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
                               : launch(full_kernel<uint16_t, 8, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);

@@ -19,6 +19,7 @@ arguments, allocates outputs with torch and launches on the current HIP stream.
 from __future__ import annotations
 
 import math
+import threading
 from dataclasses import dataclass
 from typing import Optional
 
@@ -229,6 +230,9 @@ def sample_next(logits: torch.Tensor, temperature: float,
     row = logits.reshape(1, -1) if logits.ndim == 1 else logits
     if row.ndim != 2 or row.shape[0] != 1:
         raise ValueError("model next_token_logits must return [1, vocabulary_size]")
+    if draw == "inverse_cdf" and not knobs and isinstance(row, torch.Tensor) and row.is_cuda and \
+            row.dtype in (torch.float32, torch.bfloat16) and row.stride(1) == 1 and row.shape[1] > 0:
+        return _next_step(row, temperature, generator)
     if draw == "exponential_race":
         if generator is not None and generator.device.type != "cpu":
             raise ValueError("generation requires a CPU torch.Generator")
@@ -239,6 +243,59 @@ def sample_next(logits: torch.Tensor, temperature: float,
     else:
         raise ValueError("draw must be 'inverse_cdf' or 'exponential_race'")
     return int(result.ids.item()), float(result.logprobs.item())
+
+
+class _StepBuffers:
+    """The batch-1 sampling step's buffers for one (device, dtype, vocabulary): a 32-byte
+    pinned host block the kernel reads its uniform from and writes its outputs to (id int64,
+    log-prob fp32, kept int32, status int32, uniform fp32), the device workspace and the
+    descriptor.  One synchronisation per token, no copies and no allocations."""
+
+    def __init__(self, row: torch.Tensor):
+        self.host = torch.zeros(8, dtype=torch.int32, pin_memory=True)
+        self.i64 = self.host.numpy().view("int64")
+        self.i32 = self.host.numpy()
+        self.f32 = self.host.numpy().view("float32")
+        base = self.host.data_ptr()
+        desc = _rows_desc(row, None, None, 1.0, 1.0, 0.0, 0.0, 0, 1.0, 0.0)
+        desc.uniforms = base + 20
+        desc.out_ids, desc.out_logprob, desc.out_kept, desc.out_status = base, base + 8, base + 12, base + 16
+        self.desc = desc
+        self.lib = _lib.load()
+        self.ws_bytes = self.lib.dsv41_sampler_workspace_bytes(_lib.ctypes.byref(desc))
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=row.device)
+        self.lock = threading.Lock()  # callers on several threads take turns on the block
+
+
+_step_buffers: dict = {}
+
+
+def _next_step(row: torch.Tensor, temperature: float, generator: Optional[torch.Generator]) -> tuple[int, float]:
+    """sample_next's inverse-CDF step on one GPU row without further knobs: the kernels of
+    :func:`sample` (so the same token and log-prob bit for bit) with the uniform taken from
+    the generator as ``sample`` takes it."""
+    validate_temperature(temperature)
+    if generator is not None and generator.device.type != "cpu":
+        raise ValueError("generation requires a CPU torch.Generator")
+    key = (row.device, row.dtype, row.shape[1], row.stride(0), row.data_ptr() % 16 == 0)
+    buf = _step_buffers.get(key)
+    if buf is None:
+        buf = _step_buffers[key] = _StepBuffers(row)
+    u = float(torch.rand(1, generator=generator, dtype=torch.float32)[0])
+    with buf.lock, torch.cuda.device(row.device):
+        buf.f32[5] = u
+        buf.i32[4] = -1
+        d = buf.desc
+        d.logits = row.data_ptr()
+        d.temperature = temperature
+        stream = torch.cuda.current_stream(row.device)
+        rc = buf.lib.dsv41_sampler_run(_lib.ctypes.byref(d), buf.ws.data_ptr(), buf.ws_bytes, stream.cuda_stream)
+        _lib.check(rc)
+        stream.synchronize()
+        status, token, lp = int(buf.i32[4]), int(buf.i64[0]), float(buf.f32[2])
+    if status:
+        _status_error(torch.tensor([status]))
+    return token, lp
 
 
 @dataclass
