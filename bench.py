@@ -40,7 +40,8 @@ BF16_PEAK_TFLOPS = 2500.0
 # counts are in the profiles/ summaries of each kernel and workload.
 MEASURED_TRAFFIC = {
     "sampler_E": 2_629_506_528 + 1_937_544,  # topk_kernel + select_kernel
-    "sampler_B": 160_335_872 + 32_768,  # full_kernel (profiles/sampler_full_B.md)
+    "sampler_B": 83_307_725 + 32_768,  # full_kernel (profiles/sampler_full_B.md)
+    "sampler_E_full": 2_494_241_178 + 17_311_130,  # full_kernel (profiles/sampler_full_E_shape.md)
     "sampler_A": 5_004_270 + 393_216 + 79_872,  # sliced topk_kernel + merge_kernel
     "logprob_D": 46_112_195_686 + 1_048_576,
     "logprob_C": 7_592_285_070 + 1_245_184,  # fused_kernel + merge_kernel
@@ -59,7 +60,7 @@ def parse():
     # steady state (20 steps after 5 read several percent slow on a fresh box).
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="E", choices=["A", "B", "E", "none"],
+    ap.add_argument("--workload", default="E", choices=["A", "B", "E", "E_full", "none"],
                     help="headline sampler config; 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
     ap.add_argument("--logprob-steps", type=int, default=10)
@@ -92,14 +93,20 @@ def copy_calibration(nbytes, steps, torch):
     print(json.dumps({"copy_bytes": nbytes, "ms": ms, "GBps": 2 * nbytes / ms / 1e6}), flush=True)
 
 
-def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0):
+def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0, full=False):
+    """One sampler configuration.  ``full``: the training-default mode on the configuration's
+    logits (rollout_manager/training.py:74-81): the temperature alone, no penalties and no
+    truncation, so a full-vocabulary inverse-CDF draw."""
     from dsv41_rocm import _lib, workloads
 
-    cfg = workloads.SAMPLER_CONFIGS[name]
     dev = torch.device("cuda:0")
     print(f"[bench] generating sampler config {name} on the GPU", file=sys.stderr, flush=True)
     inp = workloads.sampler_inputs(name, device=dev)
     logits, history, uniforms, knobs = inp["logits"], inp["history"], inp["uniforms"], inp["knobs"]
+    if full:
+        knobs = {"temperature": knobs.get("temperature", 1.0)}
+        history = history[:, :0]
+        inp = dict(inp, history=history, knobs=knobs)
     rows, vocab = logits.shape
     ids = torch.empty(rows, dtype=torch.int64, device=dev)
     lps = torch.empty(rows, dtype=torch.float32, device=dev)
@@ -111,9 +118,10 @@ def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0):
     d.logits_dtype = _lib.DTYPE_F32 if logits.dtype == torch.float32 else _lib.DTYPE_BF16
     d.logits_row_stride = logits.stride(0)
     d.logits = logits.data_ptr()
-    d.history = history.data_ptr()
-    d.history_row_stride = history.stride(0)
-    d.hist_len = history.shape[1]
+    if history.shape[1]:
+        d.history = history.data_ptr()
+        d.history_row_stride = history.stride(0)
+        d.hist_len = history.shape[1]
     d.uniforms = uniforms.data_ptr()
     d.temperature = knobs.get("temperature", 1.0)
     d.repetition_penalty = knobs.get("repetition_penalty", 1.0)
@@ -158,10 +166,12 @@ def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0):
         "dtype": "f32" if esize == 4 else "bf16",
         "data": "synthetic",
         "config": {"workload": f"{name}: sampler {rows}x{vocab} "
-                               f"{'fp32' if esize == 4 else 'bf16'}, history {history.shape[1]}",
+                               f"{'fp32' if esize == 4 else 'bf16'}, history {history.shape[1]}"
+                               + (", training-default full-vocabulary inverse CDF" if full else ""),
                    "rows": rows, "vocab": vocab, "hist_len": history.shape[1], **knobs},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": MEASURED_TRAFFIC.get(f"sampler_{name}"),
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": MEASURED_TRAFFIC.get(f"sampler_{name}" + ("_full" if full else "")),
                      "bytes_per_row": per_row},
         "steady_state": {"steps": steady_steps, "ms_per_step": steady_ms,
                          "rows_per_s": rows / (steady_ms * 1e-3),
@@ -234,7 +244,8 @@ def main():
     if args.workload == "none":
         line = {}
     else:
-        line = bench_sampler(args.workload, args.steps, args.warmup, cpu, torch)
+        line = bench_sampler(args.workload.split("_")[0], args.steps, args.warmup, cpu, torch,
+                             full=args.workload.endswith("_full"))
         print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
         line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 3, cpu, torch,
@@ -245,6 +256,8 @@ def main():
             if name != args.workload:
                 extra[f"sampler_{name}"] = bench_sampler(name, 200, 20, cpu, torch, cpu_seconds=4.0)
                 print(json.dumps({name: extra[f"sampler_{name}"]["ms_per_step"]}), file=sys.stderr, flush=True)
+        extra["sampler_E_full"] = bench_sampler("E", 100, 20, cpu, torch, cpu_seconds=4.0, full=True)
+        print(json.dumps({"E_full": extra["sampler_E_full"]["ms_per_step"]}), file=sys.stderr, flush=True)
         if args.logprob != "C":
             extra["logprob_C"] = bench_logprob("C", 20, 3, cpu, torch, backward=False)
         extra["decode_B1"] = bench_decode(torch)
