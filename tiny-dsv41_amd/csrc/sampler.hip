@@ -1067,7 +1067,10 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   float* penz = reinterpret_cast<float*>(smem + L.penx);
   const int NC = n_chunks<G>(p.V);
   const int NE = n_mass_chunks(p.V);
-  uint64_t* cq = reinterpret_cast<uint64_t*>(smem + L.mode0);  // exact masses of the 256-id chunks
+  // exact masses of the 256-id chunks: during the stream fp64 sums of integers below 2^51
+  // (exact in any order), then the u64 chunk weights
+  uint64_t* cq = reinterpret_cast<uint64_t*>(smem + L.mode0);
+  double* cqd = reinterpret_cast<double*>(cq);
   float* em = reinterpret_cast<float*>(cq + NE);  // 256-id chunk maxima over ids outside the history
   float* cs = em + NE;                            // wave-span sums of exp(z - span maximum)
   // the maximum of wave span c: one 256-id chunk (G = 4) or two (G = 8)
@@ -1098,7 +1101,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     for (int c = tid; c < NC; c += NT) cs[c] = pcs[c];
     for (int e = tid; e < NE; e += NT) {
       em[e] = pem[e];
-      if constexpr (EXACT) cq[e] = pw[e];
+      if constexpr (EXACT) cqd[e] = (double)pw[e];
     }
     for (int s = tid; s < p.n_slices; s += NT) bad |= p.pre_st[(int64_t)row * p.n_slices + s];
     __syncthreads();  // status cleared before any thread sets a bit
@@ -1134,8 +1137,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
             if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) em[e] = mc;
             // rows 0 + 1 (and 2 + 3) are one chunk: each row's lane 0 adds its total
             if constexpr (EXACT)
-              if ((lane & 15) == 0 && e < NE)
-                atomicAdd(reinterpret_cast<unsigned long long*>(&cq[e]), (unsigned long long)rs4);
+              if ((lane & 15) == 0 && e < NE) atomicAdd(&cqd[e], rs4);
             const int c = t * NW + wid;
             if (lane == 0 && c < NC) cs[c] = s;
           }
@@ -1354,7 +1356,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   }
   if constexpr (EXACT) {
     for (int c = tid; c < NE; c += NT) {
-      uint64_t q = scale_mass(cq[c], mass_ff(em[c], Mref));
+      uint64_t q = scale_mass((uint64_t)cqd[c], mass_ff(em[c], Mref));
       if (p.has_pen) {
         const int s1 = rank_below(h, min((c + 1) * MASS_CHUNK, p.V), p.words, U);
         for (int s = rank_below(h, c * MASS_CHUNK, p.words, U); s < s1; ++s) q += mass_of(penz[s], Mref);
