@@ -179,7 +179,8 @@ typedef struct dsv41_sampler_shard_desc {
 typedef struct dsv41_full_state {
   float max_z;      /* the slice's largest processed logit; -inf when it has none */
   int32_t status;   /* DSV41_STATUS_* bits seen by this slice */
-  double mass;      /* sum over the slice of exp(z - max_z), in the slice's fixed chunk order */
+  double mass;      /* sum over the slice of exp(z - max_z): its exact fixed-point masses
+                       against max_z (integers, as dsv41_sampler_run forms them) times 2^-43 */
   int64_t argmax;   /* global id of the slice's first largest logit */
   int64_t reserved;
 } dsv41_full_state;

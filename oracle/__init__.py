@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
                                            ctypes.POINTER(ctypes.c_uint32)]
         c.dsv41_oracle_sample.restype = ctypes.c_int
         c.dsv41_oracle_full_draw.restype = ctypes.c_int64
+        c.dsv41_oracle_full_total.restype = ctypes.c_uint64
         _lib = c
     return _lib
 
@@ -114,6 +115,19 @@ def full_draw(z, U: int, *, history_ids=None, slice_starts=None) -> int:
     ss = None if slice_starts is None else np.ascontiguousarray(np.asarray(slice_starts, dtype=np.int32))
     return int(lib().dsv41_oracle_full_draw(_ptr(z), ctypes.c_int(z.shape[0]), _ptr(counts), _ptr(ss),
                                             ctypes.c_int(0 if ss is None else ss.size), ctypes.c_uint32(U)))
+
+
+def full_total(z, *, history_ids=None, slice_starts=None) -> int:
+    """The exact total S of the full-vocabulary draw's 2^-43 masses over processed logits
+    ``z``: every full-vocabulary draw reports lp = (z_tok - max z) - log(S 2^-43)."""
+    z = np.ascontiguousarray(np.asarray(z, dtype=np.float32))
+    counts = None
+    if history_ids is not None:
+        counts = np.zeros(z.shape[0], np.uint32)
+        counts[np.asarray(history_ids, dtype=np.int64)] = 1
+    ss = None if slice_starts is None else np.ascontiguousarray(np.asarray(slice_starts, dtype=np.int32))
+    return int(lib().dsv41_oracle_full_total(_ptr(z), ctypes.c_int(z.shape[0]), _ptr(counts), _ptr(ss),
+                                             ctypes.c_int(0 if ss is None else ss.size)))
 
 
 def check_division(temperature: float, lo: int, hi: int) -> tuple[int, int]:

@@ -201,46 +201,75 @@ int dsv41_oracle_process_row(const float* x, int V, const int64_t* hist, int hle
  * owes names the token.  Every quantity is an integer, so sums in any order agree.
  */
 #define MASS_CHUNK 256
+/* The chunk [lo, hi)'s maximum over ids outside H (mc), its g and its weight Q. */
+static uint64_t chunk_weight(const float* z, int lo, int hi, const uint32_t* counts, float zmax, float* mc_out,
+                             uint64_t* g_out) {
+  float mc = -INFINITY;
+  for (int v = lo; v < hi; ++v)
+    if (!(counts && counts[v]) && z[v] > mc) mc = z[v];
+  const uint64_t g = dsv41_mass(mc, zmax);
+  uint64_t W = 0, Hm = 0;
+  for (int v = lo; v < hi; ++v) {
+    if (counts && counts[v]) Hm += dsv41_mass(z[v], zmax);
+    else W += dsv41_mass(z[v], mc);
+  }
+  *mc_out = mc;
+  *g_out = g;
+  return (uint64_t)(((u128)W * g) >> 43) + Hm;
+}
+
+/* S = sum Q_c over the chunks of every slice: the total every full-vocabulary draw reports
+ * its log-prob against, lp = (z_tok - zmax) - log(S 2^-43). */
+static uint64_t full_total(const float* z, int V, const uint32_t* counts, const int32_t* starts, int n_starts,
+                           float zmax) {
+  uint64_t S = 0;
+  for (int s = 0; s < (starts ? n_starts : 1); ++s) {
+    const int a = starts ? starts[s] : 0;
+    const int b = (starts && s + 1 < n_starts) ? starts[s + 1] : V;
+    for (int lo = a; lo < b; lo += MASS_CHUNK) {
+      float mc;
+      uint64_t g;
+      S += chunk_weight(z, lo, lo + MASS_CHUNK < b ? lo + MASS_CHUNK : b, counts, zmax, &mc, &g);
+    }
+  }
+  return S;
+}
+
 static int64_t full_draw(const float* z, int V, const uint32_t* counts, const int32_t* starts, int n_starts,
                          float zmax, uint64_t U) {
-  /* chunk list: [lo, hi) per chunk; a first pass for S, a second for the token */
-  uint64_t S = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    uint64_t t = 0, before = 0;
-    if (pass == 1) t = (uint64_t)(((u128)S * U) >> 32); /* dsv41_draw_target with U = u 2^32 */
-    for (int s = 0; s < (starts ? n_starts : 1); ++s) {
-      const int a = starts ? starts[s] : 0;
-      const int b = (starts && s + 1 < n_starts) ? starts[s + 1] : V;
-      for (int lo = a; lo < b; lo += MASS_CHUNK) {
-        const int hi = lo + MASS_CHUNK < b ? lo + MASS_CHUNK : b;
-        float mc = -INFINITY;
-        for (int v = lo; v < hi; ++v)
-          if (!(counts && counts[v]) && z[v] > mc) mc = z[v];
-        const uint64_t g = dsv41_mass(mc, zmax);
-        uint64_t W = 0, Hm = 0;
+  const uint64_t S = full_total(z, V, counts, starts, n_starts, zmax);
+  const uint64_t t = (uint64_t)(((u128)S * U) >> 32); /* dsv41_draw_target with U = u 2^32 */
+  uint64_t before = 0;
+  for (int s = 0; s < (starts ? n_starts : 1); ++s) {
+    const int a = starts ? starts[s] : 0;
+    const int b = (starts && s + 1 < n_starts) ? starts[s + 1] : V;
+    for (int lo = a; lo < b; lo += MASS_CHUNK) {
+      const int hi = lo + MASS_CHUNK < b ? lo + MASS_CHUNK : b;
+      float mc;
+      uint64_t g;
+      const uint64_t Q = chunk_weight(z, lo, hi, counts, zmax, &mc, &g);
+      if (t < before + Q) {
+        const uint64_t need = t - before;
+        uint64_t cw = 0, ch = 0;
         for (int v = lo; v < hi; ++v) {
-          if (counts && counts[v]) Hm += dsv41_mass(z[v], zmax);
-          else W += dsv41_mass(z[v], mc);
+          if (counts && counts[v]) ch += dsv41_mass(z[v], zmax);
+          else cw += dsv41_mass(z[v], mc);
+          if (need < (uint64_t)(((u128)cw * g) >> 43) + ch) return v;
         }
-        const uint64_t Q = (uint64_t)(((u128)W * g) >> 43) + Hm;
-        if (pass == 0) {
-          S += Q;
-          continue;
-        }
-        if (t < before + Q) {
-          const uint64_t need = t - before;
-          uint64_t cw = 0, ch = 0;
-          for (int v = lo; v < hi; ++v) {
-            if (counts && counts[v]) ch += dsv41_mass(z[v], zmax);
-            else cw += dsv41_mass(z[v], mc);
-            if (need < (uint64_t)(((u128)cw * g) >> 43) + ch) return v;
-          }
-        }
-        before += Q;
       }
+      before += Q;
     }
   }
   return -1; /* no mass: only rows without a finite maximum */
+}
+
+/* The exact total S of processed logits z[V] (maximum taken over z). */
+uint64_t dsv41_oracle_full_total(const float* z, int V, const uint32_t* counts, const int32_t* starts,
+                                 int n_starts) {
+  float zmax = z[0];
+  for (int v = 1; v < V; ++v)
+    if (z[v] > zmax) zmax = z[v];
+  return full_total(z, V, counts, starts, n_starts, zmax);
 }
 
 /* The full-vocabulary inverse-CDF draw of processed logits z[V] against the 32-bit

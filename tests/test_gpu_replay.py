@@ -6,9 +6,11 @@ drawn token, whichever draw produced it; and it must agree with torch's
 log_softmax(logits / T)[token] within 1e-5 where no penalties apply.
 """
 
+import numpy as np
 import pytest
 import torch
 
+import oracle
 from dsv41_rocm import replay_log_probs, sample, workloads
 
 pytestmark = pytest.mark.gpu
@@ -34,6 +36,37 @@ def test_replay_equals_behaviour_bitwise(name, rows, draw):
         res = sample(x, history=h, generator=g, **pen)
     lp = replay_log_probs(x, res.ids, history=h, **pen)
     assert torch.equal(lp, res.logprobs)
+
+
+@pytest.mark.parametrize("draw", ["cdf", "race", "greedy"])
+def test_log_prob_is_against_the_exact_mass_total(draw):
+    """Every full-vocabulary draw reports lp = (z_tok - M) - log(S 2^-43), S the exact
+    integer total of the draw's 2^-43 masses: the float equals the one formed from the
+    oracle's processed row and its S (the fp64 logs of the two sides agree far below the
+    float's rounding), on config B's rows with their penalties."""
+    inp = workloads.sampler_inputs("B", rows=24)
+    x, h, knobs = inp["logits"], inp["history"], inp["knobs"]
+    print(f"case: config B rows 24 draw {draw}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    kw = {}
+    if draw == "race":
+        kw["exponentials"] = torch.empty(x.shape, dtype=torch.float32).exponential_(1, generator=g).to(DEV)
+    elif draw == "greedy":
+        kw["greedy"] = True
+    else:
+        kw["uniforms"] = inp["uniforms"].to(DEV)
+    res = sample(x.to(DEV), history=h.to(DEV), **knobs, **kw)
+    ids, lps = res.ids.cpu().numpy(), res.logprobs.cpu().numpy()
+    assert (res.status.cpu() == 0).all()
+    xf = x.float().numpy()
+    for r in range(x.shape[0]):
+        z, st = oracle.process_row(xf[r], temperature=knobs["temperature"], history=h[r].numpy(),
+                                   presence_penalty=knobs["presence_penalty"],
+                                   frequency_penalty=knobs["frequency_penalty"])
+        assert st == 0
+        S = oracle.full_total(z, history_ids=np.unique(h[r].numpy()))
+        want = np.float32((np.float64(z[ids[r]]) - np.float64(z.max())) - np.log(float(S) * 2.0**-43))
+        assert lps[r] == want, (r, lps[r], want)
 
 
 def test_replay_matches_torch_log_softmax_and_any_token():

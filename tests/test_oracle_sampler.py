@@ -347,6 +347,45 @@ def test_full_draw_intervals_are_the_softmax(case):
         assert np.array_equal(lengths, _draw_intervals(z))
 
 
+@pytest.mark.parametrize("case", ["plain", "history", "slices_aligned", "slices_ragged"])
+def test_full_total_is_the_softmax_normalizer(case):
+    """The exact total S every full-vocabulary draw reports its log-prob against:
+    S 2^-43 = sum exp(z - zmax) within fp32 accuracy on rows whose chunks sit at different
+    heights (+3, 0, -5, -60), so a missing or wrong chunk scale is off by a factor e^3 or
+    more and a dropped history mass by the history's share (the row maximum is on a history
+    id).  Slices cut at multiples of 256 are the unsliced chunks: the same integer."""
+    g = np.random.default_rng(23)
+    z = (2.0 * g.standard_normal(900)).astype(np.float32)
+    z[:256] += 3.0
+    z[512:768] -= 5.0
+    z[768:] -= 60.0
+    kw = {}
+    if case == "history":
+        hist = g.choice(900, size=60, replace=False)
+        hist[0] = int(np.argmax(z))
+        kw["history_ids"] = hist
+    if case == "slices_aligned":
+        kw["slice_starts"] = [0, 256, 768]
+    if case == "slices_ragged":
+        kw["slice_starts"] = [0, 301, 611]
+    S = oracle.full_total(z, **kw)
+    e = np.exp(z.astype(np.float64) - float(z.max())).sum()
+    assert abs(S * 2.0**-43 - e) <= 2e-6 * e
+    if case == "slices_aligned":
+        assert S == oracle.full_total(z)
+
+
+def test_full_total_single_chunk_is_the_sum_of_masses():
+    """At most 256 ids without history: one chunk whose maximum is the row maximum, so S is
+    the plain sum of floor(2^43 exp32(z - zmax)), and the maximum alone weighs 2^43."""
+    g = np.random.default_rng(5)
+    for V in (1, 7, 256):
+        z = (3.0 * g.standard_normal(V)).astype(np.float32)
+        zmax = float(z.max())
+        assert oracle.full_total(z) == sum(oracle.mass(float(v), zmax) for v in z)
+    assert oracle.full_total(np.array([2.5], np.float32)) == 1 << 43
+
+
 def test_full_draw_single_chunk_is_the_plain_inverse_cdf():
     """A row of at most 256 ids without history is one chunk whose maximum is the row
     maximum: its masses are floor(2^43 exp32(z - zmax)) in vocabulary order, the

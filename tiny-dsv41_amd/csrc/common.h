@@ -73,13 +73,6 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
   return fmaxf(fmaxf(rl(v, 0), rl(v, 16)), fmaxf(rl(v, 32), rl(v, 48)));
 }
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += dpp_f32<0xB1>(v);
-  v += dpp_f32<0x4E>(v);
-  v += dpp_f32<0x124>(v);
-  v += dpp_f32<0x128>(v);
-  return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
-}
 
 // inclusive prefix sums across the 64 lanes (all lanes active).  Integer sums are exact in
 // any order, so the integer scans go by DPP: shifts of 1, 2, 4 and 8 lanes within each
@@ -102,14 +95,6 @@ __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
   v += dpp_scan_u64<0x118>(v);        // row_shr:8
   v += dpp_scan_u64<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
   v += dpp_scan_u64<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
-  return v;
-}
-__device__ __forceinline__ double wave_incl_scan_d(double v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    double t = __shfl_up(v, o);
-    if (lane >= o) v += t;
-  }
   return v;
 }
 __device__ __forceinline__ int wave_incl_scan_i(int v, int lane) {

@@ -78,7 +78,6 @@ constexpr int FULL_CPOL = 0;  // full_kernel's exact draw re-reads each row: def
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr uint32_t NEG_INF_BITS = 0xFF800000u;
-constexpr float LOG2E = 1.4426950408889634f;
 
 constexpr int ST_NONFINITE = DSV41_STATUS_NONFINITE;
 constexpr int ST_BAD_HISTORY = DSV41_STATUS_BAD_HISTORY;
@@ -163,7 +162,6 @@ struct Params {
   // small FULL batch spread over the GPU: full_slice_kernel writes each row's wave-span
   // sums [rows, NC], 256-id chunk maxima and exact masses [rows, NE] and per-slice status
   // [rows, n_slices] (slice_w wave spans per slice); full_kernel<..., PRE> finishes rows
-  float* pre_cs;
   float* pre_em;
   uint64_t* pre_w;
   int32_t* pre_st;
@@ -226,7 +224,7 @@ __host__ __device__ inline Layout make_layout(int V, int words, int ucap, int ca
   l.hist256 = off;
   off += 256 * 8;
   l.mode0 = off;
-  if (MODE == MODE_FULL) off += 4 * (size_t)n_chunks<G>(V) + 12 * (size_t)n_mass_chunks(V);
+  if (MODE == MODE_FULL) off += 12 * (size_t)n_mass_chunks(V);
   if (MODE == MODE_TOPK) off += 8 * (size_t)cap;
   if (MODE == MODE_TOPP) off += 8 * ((size_t)TOPP_BINS + (size_t)n_chunks<G>(V) + (size_t)cap);
   l.total = align16(off);
@@ -966,34 +964,23 @@ __device__ __forceinline__ uint64_t scale_mass(uint64_t w, float g) {
 }
 
 // Statistics of one wave span of 64 G processed logits (lane l holds z for ids l G ..
-// l G + G - 1 of the span): mx = the span maximum; mc = the maximum of the lane's 256-id mass
-// chunk (the span, or its half: lanes 0-31 and 32-63); s = the wave sum of exp(z - mx) in
-// fp32, the same in every lane; (EXACT) rs4 = the lane's 16-lane row total of the masses
+// l G + G - 1 of the span): mc = the maximum of the lane's 256-id mass chunk (the span, or
+// its half: lanes 0-31 and 32-63); rs4 = the lane's 16-lane row total of the masses
 // floor(2^43 exp32(z - mc)), integers of at most 2^43, so the fp64 sums are exact in any
 // order (a chunk's total is below 2^51).
-template <int G, bool EXACT>
-__device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float& mx, float& mc, float& s,
-                                           double& rs4) {
-  mx = z[0];
+template <int G>
+__device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float& mc, double& rs4) {
+  float mx = z[0];
 #pragma unroll
   for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
   float rmx[4];
   row_max4(mx, rmx);
-  mx = fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
-  mc = G == 4 ? mx : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
-  if constexpr (EXACT) {
-    double qd = 0.0;
+  mc = G == 4 ? fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]))
+              : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
+  double qd = 0.0;
 #pragma unroll
-    for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
-    rs4 = row_sum_f64(qd);
-  }
-  s = 0.0f;
-  if (mx > NEG_INF) {
-    const float mb = mx * LOG2E;
-#pragma unroll
-    for (int j = 0; j < G; ++j) s += exp2f(__builtin_fmaf(z[j], LOG2E, -mb));
-  }
-  s = wave_sum_dpp(s);
+  for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
+  rs4 = row_sum_f64(qd);
 }
 
 __device__ __forceinline__ double rl_d(double v, int lane) {
@@ -1009,7 +996,7 @@ __device__ __forceinline__ double rl_d(double v, int lane) {
 // full_kernel<..., PRE> finishes each row with the values and the order of the one-workgroup
 // kernel: the same ids and log-probs, bit for bit.
 constexpr int PRE_NT = 256;
-template <typename TIn, int G, bool VEC, bool EXACT>
+template <typename TIn, int G, bool VEC>
 __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
   constexpr int NW = PRE_NT / 64;
   const int row = blockIdx.x / p.n_slices, sl = blockIdx.x % p.n_slices;
@@ -1017,7 +1004,6 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
   const int NC = n_chunks<G>(p.V), NE = n_mass_chunks(p.V);
   const int c1 = min((sl + 1) * p.slice_w, NC);
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(row_ptr<TIn>(p, row), (uint32_t)p.V * (uint32_t)sizeof(TIn));
-  float* ocs = p.pre_cs + (int64_t)row * NC;
   float* oem = p.pre_em + (int64_t)row * NE;
   uint64_t* ow = p.pre_w + (int64_t)row * NE;
   int bad = 0;
@@ -1032,20 +1018,17 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
     float x[G], z[G];
     unpack(A, x);
     make_z<G, true>(x, base, p, nullptr, z, bad);  // no penalties here; ids past V read -inf
-    float mx, mc, s;
-    double rs4 = 0.0;
-    span_stats<G, EXACT>(z, lane, mx, mc, s, rs4);
-    if (lane == 0) ocs[c] = s;
+    float mc;
+    double rs4;
+    span_stats<G>(z, lane, mc, rs4);
     const int e = c * (64 * G / MASS_CHUNK) + (G == 4 ? 0 : (lane >> 5));
     if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) oem[e] = mc;
-    if constexpr (EXACT) {
-      const double r0 = rl_d(rs4, 0), r1 = rl_d(rs4, 16), r2 = rl_d(rs4, 32), r3 = rl_d(rs4, 48);
-      if (G == 4) {
-        if (lane == 0 && e < NE) ow[e] = (uint64_t)((r0 + r1) + (r2 + r3));
-      } else {
-        if (lane == 0 && e < NE) ow[e] = (uint64_t)(r0 + r1);
-        if (lane == 32 && e < NE) ow[e] = (uint64_t)(r2 + r3);
-      }
+    const double r0 = rl_d(rs4, 0), r1 = rl_d(rs4, 16), r2 = rl_d(rs4, 32), r3 = rl_d(rs4, 48);
+    if (G == 4) {
+      if (lane == 0 && e < NE) ow[e] = (uint64_t)((r0 + r1) + (r2 + r3));
+    } else {
+      if (lane == 0 && e < NE) ow[e] = (uint64_t)(r0 + r1);
+      if (lane == 32 && e < NE) ow[e] = (uint64_t)(r2 + r3);
     }
     if (cn < c1) A = B;
     c = cn;
@@ -1055,8 +1038,8 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
 }
 
 // ====================================================================== FULL
-// No truncation: kept set = whole vocabulary.  Chunk c = [c*64G, (c+1)*64G) is one
-// wave's span of one tile; its (max, sum exp(z - max)) go to LDS.
+// No truncation: kept set = whole vocabulary.  Span c = [c*64G, (c+1)*64G) is one wave's
+// span of one tile; the exact masses of its one or two 256-id chunks go to LDS.
 template <typename TIn, int G, bool VEC, int DRAW, bool PRE = false>
 __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
@@ -1072,7 +1055,6 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   uint64_t* cq = reinterpret_cast<uint64_t*>(smem + L.mode0);
   double* cqd = reinterpret_cast<double*>(cq);
   float* em = reinterpret_cast<float*>(cq + NE);  // 256-id chunk maxima over ids outside the history
-  float* cs = em + NE;                            // wave-span sums of exp(z - span maximum)
   // the maximum of wave span c: one 256-id chunk (G = 4) or two (G = 8)
   auto span_max = [&](int c) {
     if (G == 4) return em[c];
@@ -1080,10 +1062,10 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   };
   constexpr bool SLICE = DRAW == DRAW_STATE || DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_RACE ||
                          DRAW == DRAW_SHARD_MASS;
-  // Inverse-CDF draws take exact fixed-point masses (see below) in the same pass as the
-  // maximum: w_i = floor(2^43 exp32(z_i - m_c)) against the maximum m_c of the token's
-  // 256-id chunk, summed exactly per chunk.
-  constexpr bool EXACT = DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_MASS;
+  // Every draw takes exact fixed-point masses (see below) in the same pass as the maximum:
+  // w_i = floor(2^43 exp32(z_i - m_c)) against the maximum m_c of the token's 256-id chunk,
+  // summed exactly per chunk.  The inverse-CDF draws place their target in them.
+  constexpr bool PLACES = DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF;
   static_assert(64 * G == MASS_CHUNK || 64 * G == 2 * MASS_CHUNK, "a wave span holds one or two mass chunks");
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -1095,13 +1077,11 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   if constexpr (PRE) {
     // the span statistics full_slice_kernel formed (no penalties on this path)
     if (tid == 0) m->status = 0;
-    const float* pcs = p.pre_cs + (int64_t)row * NC;
     const float* pem = p.pre_em + (int64_t)row * NE;
     const uint64_t* pw = p.pre_w + (int64_t)row * NE;
-    for (int c = tid; c < NC; c += NT) cs[c] = pcs[c];
     for (int e = tid; e < NE; e += NT) {
       em[e] = pem[e];
-      if constexpr (EXACT) cqd[e] = (double)pw[e];
+      cqd[e] = (double)pw[e];
     }
     for (int s = tid; s < p.n_slices; s += NT) bad |= p.pre_st[(int64_t)row * p.n_slices + s];
     __syncthreads();  // status cleared before any thread sets a bit
@@ -1112,8 +1092,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
-        if constexpr (EXACT)
-          for (int e = tid; e < NE; e += NT) cq[e] = 0;
+        for (int e = tid; e < NE; e += NT) cq[e] = 0;
         __syncthreads();
         if (p.has_pen) U = build_history<NT, HR, SLICE>(p, row, hi, h, m);
         landed(hi);  // the ids are read under conditions; end their loads on every path
@@ -1129,17 +1108,14 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
             unpack(R[k], x);
             if ((t + 1) * TILE <= p.V) make_z<G, false>(x, base, p, h.bitmap, z, bad);
             else make_z<G, true>(x, base, p, h.bitmap, z, bad);
-            float mx, mc, s;
-            double rs4 = 0.0;
-            span_stats<G, EXACT>(z, lane, mx, mc, s, rs4);
+            float mc;
+            double rs4;
+            span_stats<G>(z, lane, mc, rs4);
             // the lane's 256-id chunk: the span, or its half for G = 8
             const int e = (t * TILE + wid * 64 * G) / MASS_CHUNK + (G == 4 ? 0 : (lane >> 5));
             if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) em[e] = mc;
             // rows 0 + 1 (and 2 + 3) are one chunk: each row's lane 0 adds its total
-            if constexpr (EXACT)
-              if ((lane & 15) == 0 && e < NE) atomicAdd(&cqd[e], rs4);
-            const int c = t * NW + wid;
-            if (lane == 0 && c < NC) cs[c] = s;
+            if ((lane & 15) == 0 && e < NE) atomicAdd(&cqd[e], rs4);
           }
         }
         for (int i = tid; i < n; i += NT) {
@@ -1160,37 +1136,55 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   for (int c = tid; c < NE; c += NT) cmax = fmaxf(cmax, em[c]);
   const float M = block_max<NT>(fmaxf(pmax, cmax), m);
 
-  // rescale chunk sums to the row maximum and add the chunk's history tokens: their slots
-  // are in id order, so a chunk's slots are one run, summed in order by one thread
-  for (int c = tid; c < NC; c += NT) {
-    const float sm = span_max(c);
-    float v = sm > NEG_INF ? cs[c] * exp2f((sm - M) * LOG2E) : 0.0f;
-    if (p.has_pen) {
-      const int s1 = rank_below(h, min((c + 1) * 64 * G, p.V), p.words, U);
-      for (int s = rank_below(h, c * 64 * G, p.words, U); s < s1; ++s) v += exp2f((penz[s] - M) * LOG2E);
-    }
-    cs[c] = v;
+  // The draws use 2^-43 fixed-point masses, exact integers, so neither the drawn id nor
+  // the reported log-prob depends on the order of any reduction.  The row (or slice) is cut
+  // into 256-id chunks.  In the stream, an id outside the history got
+  // w_i = floor(2^43 exp32(z_i - m_c)) against its chunk's maximum m_c over such ids, and
+  // cqd[c] = W_c = sum w_i.  With the row's maximum Mref known (a slice of a sharded
+  // inverse-CDF draw: the maximum over all slices), the chunk weighs
+  //   Q_c = floor(W_c g_c / 2^43),  g_c = floor(2^43 exp32(m_c - Mref)),
+  // plus the history ids' masses floor(2^43 exp32(z_h - Mref)) (their slots are in id order,
+  // so a chunk's slots are one run, summed by one thread); the oracle defines the same
+  // integers.  S = sum Q_c is the row's total: every draw, the replay included, reports
+  // lp = (z_tok - M) - log(S 2^-43), so DRAW_REPLAY of a drawn token returns the same float
+  // bit for bit.
+  constexpr bool SHARDED = DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_MASS;
+  float Mref = M;
+  if constexpr (SHARDED) {
+    double Sg;
+    combine_states(p.sh_states, p.n_shards, p.nrows, row, Mref, Sg);
   }
-  __syncthreads();
-
-  // Row total over the chunk table in one fixed order (lane l of wave 0 sums a contiguous
-  // run of chunks, then a wave scan): every draw reports its log-prob against this total,
-  // so that DRAW_REPLAY of the drawn token returns the same float bit for bit.
-  auto chunk_total = [&](double& incl, double& own) {
-    const int per = (NC + 63) / 64;
-    const int b = lane * per, e = min(b + per, NC);
-    double s = 0.0;
-    for (int c = b; c < e; ++c) s += (double)cs[c];
+  if constexpr (DRAW != DRAW_SHARD_RACE) {  // the race over slices takes the gathered states
+    for (int c = tid; c < NE; c += NT) {
+      uint64_t q = scale_mass((uint64_t)cqd[c], mass_ff(em[c], Mref));
+      if (p.has_pen) {
+        const int s1 = rank_below(h, min((c + 1) * MASS_CHUNK, p.V), p.words, U);
+        for (int s = rank_below(h, c * MASS_CHUNK, p.words, U); s < s1; ++s) q += mass_of(penz[s], Mref);
+      }
+      cq[c] = q;
+    }
+    __syncthreads();
+  }
+  // S in wave 0: lane l sums the contiguous run of chunks [b, e), then a wave scan (every
+  // lane returns S, `own` its run and `incl` the run's inclusive prefix)
+  const int run = (NE + 63) / 64;
+  const int rb = min(lane * run, NE), re = min(rb + run, NE);
+  auto mass_scan = [&](uint64_t& own, uint64_t& incl) {
+    uint64_t s = 0;
+    for (int c = rb; c < re; ++c) s += cq[c];
     own = s;
-    incl = wave_incl_scan_d(s, lane);
+    incl = wave_incl_scan_u64(s, lane);
     return __shfl(incl, 63);
+  };
+  auto row_lp = [&](float ztok, uint64_t S) {
+    return (float)(((double)ztok - (double)M) - log((double)S * 0x1p-43));
   };
 
   if constexpr (DRAW == DRAW_REPLAY) {
     // the given token's processed log-prob (a separate instantiation, like the race)
     if (wid == 0) {
-      double incl, own;
-      const double S = chunk_total(incl, own);
+      uint64_t own, incl;
+      const uint64_t S = mass_scan(own, incl);
       if (lane == 0) {
         const int64_t tok = p.replay[row];
         float lp = __builtin_nanf("");
@@ -1198,7 +1192,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
           const int t = (int)tok;
           const bool pen = p.has_pen && ((h.bitmap[t >> 5] >> (t & 31)) & 1u);
           const float ztok = pen ? penz[slot_of(h, t)] : load_one<TIn>(rs, t) / p.T;
-          lp = (float)(((double)ztok - (double)M) - log(S));
+          lp = row_lp(ztok, S);
         } else {
           m->status |= ST_BAD_TARGET;
         }
@@ -1216,12 +1210,19 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     // same E (its draw is exponential_ followed by argmax(p / E)); only the order of the
     // sum differs, which moves every p by the same factor and can reorder only ratios
     // within an ulp of each other.
-    __syncthreads();
-    float csum = 0.0f;
-    for (int c = tid; c < NC; c += NT) csum += cs[c];
-    double S = (double)block_sum_d<NT>((double)csum, m);
     float Mr = M;  // the row's maximum (a slice: over all slices)
-    if constexpr (DRAW == DRAW_SHARD_RACE) combine_states(p.sh_states, p.n_shards, p.nrows, row, Mr, S);
+    double S;      // the row's sum of exp(z - Mr)
+    if constexpr (DRAW == DRAW_SHARD_RACE) {
+      combine_states(p.sh_states, p.n_shards, p.nrows, row, Mr, S);
+    } else {
+      if (wid == 0) {
+        uint64_t own, incl;
+        const uint64_t St = mass_scan(own, incl);
+        if (lane == 0) m->bu[1] = St;
+      }
+      __syncthreads();
+      S = (double)m->bu[1] * 0x1p-43;
+    }
     const float lsum = Mr + logf((float)S);
     const float* erow = p.exps + (int64_t)row * p.estride;
     const __amdgpu_buffer_rsrc_t re = row_rsrc(erow, (uint32_t)p.V * 4u);
@@ -1295,44 +1296,25 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
       }
       return;
     }
-    // the log-prob against the fixed-order total, as the other draws report it
-    if (wid == 0) {
-      double incl, own;
-      const double St = chunk_total(incl, own);
-      if (lane == 0) {
-        const int bi = m->ri[0];
-        const int64_t tok = bi == 0x7FFFFFFF ? 0 : bi;
-        float ztok = M;
-        if (bi != 0x7FFFFFFF) {
-          const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
-          ztok = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
-        }
-        const float lp = (float)(((double)ztok - (double)M) - log(St));
-        write_result(p, row, m, tok, lp, p.V);
+    // the log-prob against the exact total, as the other draws report it
+    if (tid == 0) {
+      const int bi = m->ri[0];
+      const int64_t tok = bi == 0x7FFFFFFF ? 0 : bi;
+      float ztok = M;
+      if (bi != 0x7FFFFFFF) {
+        const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
+        ztok = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
       }
+      write_result(p, row, m, tok, row_lp(ztok, m->bu[1]), p.V);
     }
     return;
   }
 
-  // Inverse-CDF draws use 2^-43 fixed-point masses, exact integers, so the drawn id does
-  // not depend on the order of any reduction.  The row (or slice) is cut into 256-id
-  // chunks.  In the stream, an id outside the history got w_i = floor(2^43 exp32(z_i - m_c))
-  // against its chunk's maximum m_c over such ids, and cq[c] = W_c = sum w_i.  With the row's
-  // maximum Mref known (a slice: the maximum over all slices), the chunk weighs
-  //   Q_c = floor(W_c g_c / 2^43),  g_c = floor(2^43 exp32(m_c - Mref)),
-  // plus the history ids' masses floor(2^43 exp32(z_h - Mref)); the oracle defines the same
-  // integers.  Inside the chunk holding the target, the id boundaries in Q units are
-  // floor(prefix(w) g_c / 2^43) + prefix(history masses), in vocabulary order.  The
-  // log-prob keeps the fp32 chunk total above, which every full-vocabulary draw and the
-  // replay share.
-  constexpr bool SHARDED = DRAW == DRAW_SHARD_CDF || DRAW == DRAW_SHARD_MASS;
-  const float u = (DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF) ? row_uniform(p, row, m) : 0.0f;
-  float Mref = M;
+  // The inverse-CDF target t = (S U) >> 32 picks the first chunk whose cumulative Q exceeds
+  // it; inside that chunk the id boundaries in Q units are floor(prefix(w) g_c / 2^43) +
+  // prefix(history masses), in vocabulary order.
+  const float u = PLACES ? row_uniform(p, row, m) : 0.0f;
   uint64_t tq = 0;  // the draw's target in this workgroup's masses
-  if constexpr (SHARDED) {
-    double Sg;
-    combine_states(p.sh_states, p.n_shards, p.nrows, row, Mref, Sg);
-  }
   if constexpr (DRAW == DRAW_SHARD_CDF) {
     // Every slice finds, from the same gathered masses, the slice whose masses hold the
     // target; only that one places the token, against the target less the masses before it.
@@ -1354,17 +1336,6 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
       return;
     }
   }
-  if constexpr (EXACT) {
-    for (int c = tid; c < NE; c += NT) {
-      uint64_t q = scale_mass((uint64_t)cqd[c], mass_ff(em[c], Mref));
-      if (p.has_pen) {
-        const int s1 = rank_below(h, min((c + 1) * MASS_CHUNK, p.V), p.words, U);
-        for (int s = rank_below(h, c * MASS_CHUNK, p.words, U); s < s1; ++s) q += mass_of(penz[s], Mref);
-      }
-      cq[c] = q;
-    }
-    __syncthreads();
-  }
   if constexpr (DRAW == DRAW_SHARD_MASS) {
     // this slice's exact mass against the gathered maximum; the draw step gathers them
     if (wid == 0) {
@@ -1376,21 +1347,16 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     return;
   }
   if (wid == 0) {
-    double own, incl;
-    const double S = chunk_total(incl, own);  // the log-prob's total
-    if constexpr (EXACT) {
-      // the chunk holding the target: lane l sums a contiguous run of chunks, then a scan
-      const int per = (NE + 63) / 64;
-      const int b = lane * per, e = min(b + per, NE);
-      uint64_t s = 0;
-      for (int c = b; c < e; ++c) s += cq[c];
-      const uint64_t qincl = wave_incl_scan_u64(s, lane);
-      if constexpr (DRAW == DRAW_CDF) tq = draw_target(u, __shfl(qincl, 63));
+    uint64_t own, qincl;
+    const uint64_t S = mass_scan(own, qincl);  // the log-prob's total
+    if constexpr (PLACES) {
+      // the chunk holding the target, from the runs' prefixes
+      if constexpr (DRAW == DRAW_CDF) tq = draw_target(u, S);
       int cstar = -1;
       uint64_t need = 0;
-      uint64_t before = qincl - s;
+      uint64_t before = qincl - own;
       if (before <= tq && tq < qincl) {
-        for (int c = b; c < e; ++c) {
+        for (int c = rb; c < re; ++c) {
           if (tq < before + cq[c]) {
             cstar = c;
             need = tq - before;
@@ -1410,12 +1376,12 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
         m->bu[0] = need;
       }
     }
-    if (lane == 0) m->bd[1] = S;
+    if (lane == 0) m->bu[1] = S;
   }
   // first chunk whose maximum is the row maximum, first history token at it (greedy; a
   // uniform condition, so the block reductions inside are reached by every thread or none)
   int cfirst = NC, pfirst = 0x7FFFFFFF;
-  if (!EXACT || p.greedy) {
+  if (!PLACES || p.greedy) {
     for (int c = tid; c < NC; c += NT)
       if (span_max(c) == M) cfirst = min(cfirst, c);
     for (int s = tid; s < U; s += NT)
@@ -1425,7 +1391,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   }
 
   if (wid == 0) {
-    const double S = m->bd[1];
+    const uint64_t S = m->bu[1];
     int64_t tok = 0;
     float ztok = M;
     // one chunk re-read: z of its elements, history tokens restored from penz
@@ -1445,7 +1411,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
         }
       }
     };
-    if (!EXACT || p.greedy) {  // greedy; the state carries the first argmax
+    if (!PLACES || p.greedy) {  // greedy; the state carries the first argmax
       int best = pfirst;
       if (cfirst < NC) {
         float z[G];
@@ -1460,7 +1426,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
       }
       tok = best;
       ztok = M;
-    } else if (EXACT && m->bi[0] >= 0) {
+    } else if (PLACES && m->bi[0] >= 0) {
       // The first id of the target's chunk whose boundary in Q units exceeds what the chunk
       // owes: lanes 0 .. 256/G - 1 hold the chunk's 256 ids.  An id outside the history
       // carries w_i against the chunk maximum, a history id its mass against Mref.
@@ -1516,7 +1482,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
         dsv41_full_state st;
         st.max_z = M;
         st.status = m->status;
-        st.mass = S;
+        st.mass = (double)S * 0x1p-43;
         st.argmax = tok + p.voff;
         st.reserved = 0;
         p.sh_out_states[row] = st;
@@ -1526,8 +1492,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
         // and the finish flags the row.
         p.sh_out_picks[row] = dsv41_full_pick{m->bi[0] >= 0 ? tok + p.voff : -1, ztok, 0.0f};
       } else {
-        const float lp = (float)(((double)ztok - (double)M) - log(S));
-        write_result(p, row, m, tok, lp, p.V);
+        write_result(p, row, m, tok, row_lp(ztok, S), p.V);
       }
     }
   }
@@ -3211,7 +3176,7 @@ struct Plan {
   // small FULL batch without penalties over pre_slices slices of pre_sw wave spans per row
   // (full_slice_kernel + full_kernel<..., PRE>), with the workspace offsets of its arrays
   int pre_slices, pre_sw;
-  size_t pre_cs, pre_em, pre_w, pre_st;
+  size_t pre_em, pre_w, pre_st;
 };
 
 // shard: the descriptor describes one vocabulary slice (dsv41_sampler_shard_run); the draw
@@ -3366,8 +3331,6 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
       pl->pre_slices = S;
       pl->pre_sw = sw;
       size_t off = align16(pl->workspace);
-      pl->pre_cs = off;
-      off = align16(off + (size_t)d->rows * NC * sizeof(float));
       pl->pre_em = off;
       off = align16(off + (size_t)d->rows * NE * sizeof(float));
       pl->pre_w = off;
@@ -3451,7 +3414,6 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
     char* ws = static_cast<char*>(workspace);
     p.n_slices = pl.pre_slices;
     p.slice_w = pl.pre_sw;
-    p.pre_cs = reinterpret_cast<float*>(ws + pl.pre_cs);
     p.pre_em = reinterpret_cast<float*>(ws + pl.pre_em);
     p.pre_w = reinterpret_cast<uint64_t*>(ws + pl.pre_w);
     p.pre_st = reinterpret_cast<int32_t*>(ws + pl.pre_st);
@@ -3536,21 +3498,11 @@ static int run_presliced(const dsv41_sampler_desc* d, const Plan& pl, const Para
   const bool bf = pl.esize == 2, ex = !p.greedy;
   // no dynamic LDS (a little static LDS for the block vote): no attribute to raise
   if (bf) {
-    if (pl.vec) {
-      if (ex) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, false>), grid, block, 0, s, p);
-    } else {
-      if (ex) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, false>), grid, block, 0, s, p);
-    }
+    if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false>), grid, block, 0, s, p);
   } else {
-    if (pl.vec) {
-      if (ex) hipLaunchKernelGGL((full_slice_kernel<float, 4, true, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<float, 4, true, false>), grid, block, 0, s, p);
-    } else {
-      if (ex) hipLaunchKernelGGL((full_slice_kernel<float, 4, false, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false, false>), grid, block, 0, s, p);
-    }
+    if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((full_slice_kernel<float, 4, false>), grid, block, 0, s, p);
   }
   DSV41_HIP_CHECK(hipGetLastError());
   if (bf) {
