@@ -69,6 +69,43 @@ def test_log_prob_is_against_the_exact_mass_total(draw):
         assert lps[r] == want, (r, lps[r], want)
 
 
+@pytest.mark.parametrize("vocab", [1, 255, 256, 257, 151936, 2097151])
+def test_log_prob_total_closed_forms(vocab):
+    """The exact total in closed form.  Equal logits: every id weighs 2^43, so S = V 2^43 and
+    every draw reports lp = -log V.  Two levels (k ids at 0, the rest at -d): an all-low chunk
+    weighs its count times g = floor(2^43 exp32(-d)) exactly, and a mixed chunk holds its
+    masses unscaled, so S = k 2^43 + (V - k) g whatever the chunking, and the drawn id reports
+    z_tok - log(S 2^-43).  Ids at -60 weigh nothing.  The floats must be those of numpy's fp64
+    log, bit for bit, for the inverse CDF, the race, greedy and the replay."""
+    g = torch.Generator().manual_seed(vocab)
+    rows = 3
+    x = torch.zeros(rows, vocab)
+    k = max(1, vocab // 1000)
+    top = torch.randperm(vocab, generator=g)[:k]
+    x[1] = -7.25
+    x[1, top] = 0.0
+    x[2] = -60.0  # below the 2^-43 resolution: the low ids weigh nothing
+    x[2, top] = 0.0
+    print(f"case: vocab {vocab} top ids {k}", flush=True)
+    gm = oracle.mass(-7.25, 0.0)
+    totals = [vocab << 43, (k << 43) + (vocab - k) * gm, k << 43]  # S per row, exact integers
+    xd = x.to(DEV)
+    draws = {
+        "cdf": sample(xd, uniforms=torch.rand(rows, generator=g).to(DEV)),
+        "race": sample(xd, exponentials=torch.empty(rows, vocab).exponential_(1, generator=g).to(DEV)),
+        "greedy": sample(xd, greedy=True),
+    }
+    for name, res in draws.items():
+        ids = res.ids.cpu()
+        lp = res.logprobs.cpu().numpy()
+        assert (res.status.cpu() == 0).all(), name
+        ztok = x.gather(1, ids[:, None])[:, 0].double().numpy()
+        assert ztok[2] == 0.0, name  # the ids at -60 carry no mass
+        want = np.array([np.float32(z - np.log(float(S) * 2.0**-43)) for z, S in zip(ztok, totals)])
+        assert np.array_equal(lp, want), (name, lp, want)
+        assert torch.equal(replay_log_probs(xd, res.ids).cpu(), res.logprobs.cpu()), name
+
+
 def test_replay_matches_torch_log_softmax_and_any_token():
     g = torch.Generator().manual_seed(4)
     x = (3.0 * torch.randn(16, 50021, generator=g)).to(DEV)
