@@ -92,7 +92,7 @@ constexpr int DRAW_CDF = 0;     // inverse CDF against one uniform
 constexpr int DRAW_RACE = 1;    // exponential race against Exp(1) variates
 constexpr int DRAW_REPLAY = 2;  // no draw: the log-prob of a given token
 // vocabulary slices of a full-vocabulary draw (dsv41_sampler_full_*_run)
-constexpr int DRAW_STATE = 3;       // the slice's state: max, fixed-order mass, first argmax
+constexpr int DRAW_STATE = 3;       // the slice's state: max, exact mass total, first argmax
 constexpr int DRAW_SHARD_CDF = 4;   // inverse CDF against the gathered states
 constexpr int DRAW_SHARD_RACE = 5;  // exponential race against the gathered states
 constexpr int DRAW_SHARD_MASS = 6;  // the slice's exact fixed-point mass against the gathered maximum
