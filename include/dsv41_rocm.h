@@ -113,7 +113,9 @@ typedef struct dsv41_sampler_desc {
   float min_p;                 /* [0, 1]; 0 = off */
   int32_t greedy;              /* nonzero: argmax instead of the draw */
   int64_t* out_ids;            /* [rows] */
-  float* out_logprob;          /* [rows] */
+  float* out_logprob;          /* [rows], or NULL: no log-probs (required with replay_ids); a
+                                  greedy draw without truncation then forms no masses, only
+                                  each row's first maximum */
   int32_t* out_kept;           /* [rows] or NULL */
   int32_t* out_status;         /* [rows] */
   /* Exponential-race draw (no truncation only): token = argmax_i p_i / exponentials[r, i]
@@ -223,7 +225,7 @@ typedef struct dsv41_sampler_full_finish_desc {
   const float* uniforms;           /* inverse CDF: [rows], checked to lie in [0, 1) */
   int64_t vocab_size;
   int64_t* out_ids;                /* [rows] */
-  float* out_logprob;              /* [rows] */
+  float* out_logprob;              /* [rows] or NULL */
   int32_t* out_kept;               /* [rows] or NULL */
   int32_t* out_status;             /* [rows] */
 } dsv41_sampler_full_finish_desc;
@@ -245,7 +247,7 @@ typedef struct dsv41_sampler_merge_desc {
   float min_p;
   int32_t greedy;
   int64_t* out_ids;        /* [rows] */
-  float* out_logprob;      /* [rows] */
+  float* out_logprob;      /* [rows] or NULL */
   int32_t* out_kept;       /* [rows] or NULL */
   int32_t* out_status;     /* [rows]: the OR of the slices' bits and the uniform check */
 } dsv41_sampler_merge_desc;

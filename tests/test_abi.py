@@ -91,6 +91,10 @@ def _sampler_desc(**kw):
     (dict(replay_ids=0x7000, top_k=5), _lib.E_UNSUPPORTED, "replay_ids"),
     (dict(replay_ids=0x7000, min_p=0.1), _lib.E_UNSUPPORTED, "replay_ids"),
     (dict(replay_ids=0x7000, exponentials=0x6000, exponentials_row_stride=100), _lib.E_UNSUPPORTED, "replay_ids"),
+    (dict(out_ids=None), _lib.E_INVALID, "out_ids and out_status are required"),
+    (dict(out_status=None), _lib.E_INVALID, "out_ids and out_status are required"),
+    # log-probs are optional, except for a replay, whose only output they are
+    (dict(replay_ids=0x7000, out_logprob=None), _lib.E_INVALID, "replay_ids need out_logprob"),
 ])
 def test_sampler_rejects_bad_descriptors_before_launch(kw, code, msg):
     lib = _lib.load()

@@ -667,3 +667,34 @@ def test_small_full_batches_spread_over_the_gpu(rows, V, dtype, greedy):
         okr = ok.nonzero().flatten()
         rep = replay_log_probs(xd[:rows][okr], small.ids[okr], temperature=0.7)
         assert torch.equal(rep.view(torch.int32), small.logprobs[okr].view(torch.int32))
+
+
+@pytest.mark.parametrize("case", ["B_greedy", "small_greedy_fp32", "small_greedy_bf16", "B_cdf", "B_race",
+                                  "E_topk", "E_deferred", "A_sliced"])
+def test_sampling_without_logprobs(case):
+    """``logprobs=False`` writes no log-probs and leaves every other output as the call with
+    them: ids, kept sets and statuses bit for bit.  Greedy draws without truncation take the
+    instantiation that forms no masses, over one workgroup per row (B) and over the spread
+    small batches; the other cases cover every kernel that writes log-probs."""
+    name = case.split("_")[0]
+    g = torch.Generator().manual_seed(len(case))
+    if name == "small":
+        dt = torch.float32 if case.endswith("fp32") else torch.bfloat16
+        x = (3.0 * torch.randn(8, 151936, generator=g)).to(dt).to(DEV)
+        h, kw = None, dict(greedy=True)
+    else:
+        rows = {"B": 256, "E": 64 if case == "E_topk" else 512, "A": 8}[name]
+        inp = workloads.sampler_inputs(name, rows=rows, device=DEV)
+        x, h, kw = inp["logits"], inp["history"], dict(inp["knobs"])
+        if case == "B_greedy":
+            kw["greedy"] = True
+        elif case == "B_race":
+            kw["exponentials"] = torch.empty(x.shape, dtype=torch.float32).exponential_(1, generator=g).to(DEV)
+        else:
+            kw["uniforms"] = inp["uniforms"]
+    print(f"case: {case} shape={tuple(x.shape)} dtype={x.dtype}", flush=True)
+    full = sample(x, history=h, check=False, **kw)
+    bare = sample(x, history=h, check=False, logprobs=False, **kw)
+    assert bare.logprobs is None
+    assert torch.equal(bare.ids, full.ids) and torch.equal(bare.kept, full.kept)
+    assert torch.equal(bare.status, full.status)

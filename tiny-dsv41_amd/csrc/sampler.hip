@@ -97,6 +97,7 @@ constexpr int DRAW_SHARD_CDF = 4;   // inverse CDF against the gathered states
 constexpr int DRAW_SHARD_RACE = 5;  // exponential race against the gathered states
 constexpr int DRAW_SHARD_MASS = 6;  // the slice's exact fixed-point mass against the gathered maximum
 constexpr int DRAW_GREEDY = 7;      // first largest logit, no draw
+constexpr int DRAW_ARGMAX = 8;      // first largest logit without its log-prob: no masses
 // Exact masses of the inverse-CDF draws are formed per chunk of MASS_CHUNK consecutive ids
 // of the row (or slice), against the chunk's own maximum.
 constexpr int MASS_CHUNK = 256;
@@ -885,11 +886,11 @@ __device__ __forceinline__ void write_result(const Params& p, int row, Misc* m, 
   const int st = m->status;
   if (st & ST_NONFINITE) {
     p.out_ids[row] = -1;
-    p.out_lp[row] = __builtin_nanf("");
+    if (p.out_lp) p.out_lp[row] = __builtin_nanf("");
     if (p.out_kept) p.out_kept[row] = 0;
   } else {
     p.out_ids[row] = id;
-    p.out_lp[row] = lp;
+    if (p.out_lp) p.out_lp[row] = lp;
     if (p.out_kept) p.out_kept[row] = kept;
   }
   p.out_status[row] = st;
@@ -968,7 +969,7 @@ __device__ __forceinline__ uint64_t scale_mass(uint64_t w, float g) {
 // its half: lanes 0-31 and 32-63); rs4 = the lane's 16-lane row total of the masses
 // floor(2^43 exp32(z - mc)), integers of at most 2^43, so the fp64 sums are exact in any
 // order (a chunk's total is below 2^51).
-template <int G>
+template <int G, bool MASSES = true>
 __device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float& mc, double& rs4) {
   float mx = z[0];
 #pragma unroll
@@ -977,10 +978,12 @@ __device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float&
   row_max4(mx, rmx);
   mc = G == 4 ? fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]))
               : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
-  double qd = 0.0;
+  if constexpr (MASSES) {
+    double qd = 0.0;
 #pragma unroll
-  for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
-  rs4 = row_sum_f64(qd);
+    for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
+    rs4 = row_sum_f64(qd);
+  }
 }
 
 __device__ __forceinline__ double rl_d(double v, int lane) {
@@ -996,7 +999,7 @@ __device__ __forceinline__ double rl_d(double v, int lane) {
 // full_kernel<..., PRE> finishes each row with the values and the order of the one-workgroup
 // kernel: the same ids and log-probs, bit for bit.
 constexpr int PRE_NT = 256;
-template <typename TIn, int G, bool VEC>
+template <typename TIn, int G, bool VEC, bool MASSES = true>
 __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
   constexpr int NW = PRE_NT / 64;
   const int row = blockIdx.x / p.n_slices, sl = blockIdx.x % p.n_slices;
@@ -1019,16 +1022,18 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
     unpack(A, x);
     make_z<G, true>(x, base, p, nullptr, z, bad);  // no penalties here; ids past V read -inf
     float mc;
-    double rs4;
-    span_stats<G>(z, lane, mc, rs4);
+    double rs4 = 0.0;
+    span_stats<G, MASSES>(z, lane, mc, rs4);
     const int e = c * (64 * G / MASS_CHUNK) + (G == 4 ? 0 : (lane >> 5));
     if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) oem[e] = mc;
-    const double r0 = rl_d(rs4, 0), r1 = rl_d(rs4, 16), r2 = rl_d(rs4, 32), r3 = rl_d(rs4, 48);
-    if (G == 4) {
-      if (lane == 0 && e < NE) ow[e] = (uint64_t)((r0 + r1) + (r2 + r3));
-    } else {
-      if (lane == 0 && e < NE) ow[e] = (uint64_t)(r0 + r1);
-      if (lane == 32 && e < NE) ow[e] = (uint64_t)(r2 + r3);
+    if constexpr (MASSES) {
+      const double r0 = rl_d(rs4, 0), r1 = rl_d(rs4, 16), r2 = rl_d(rs4, 32), r3 = rl_d(rs4, 48);
+      if (G == 4) {
+        if (lane == 0 && e < NE) ow[e] = (uint64_t)((r0 + r1) + (r2 + r3));
+      } else {
+        if (lane == 0 && e < NE) ow[e] = (uint64_t)(r0 + r1);
+        if (lane == 32 && e < NE) ow[e] = (uint64_t)(r2 + r3);
+      }
     }
     if (cn < c1) A = B;
     c = cn;
@@ -1066,6 +1071,8 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   // w_i = floor(2^43 exp32(z_i - m_c)) against the maximum m_c of the token's 256-id chunk,
   // summed exactly per chunk.  The inverse-CDF draws place their target in them.
   constexpr bool PLACES = DRAW == DRAW_CDF || DRAW == DRAW_SHARD_CDF;
+  // a greedy draw whose log-prob nobody asked for needs the maxima alone
+  constexpr bool MASSES = DRAW != DRAW_ARGMAX;
   static_assert(64 * G == MASS_CHUNK || 64 * G == 2 * MASS_CHUNK, "a wave span holds one or two mass chunks");
 
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -1081,7 +1088,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     const uint64_t* pw = p.pre_w + (int64_t)row * NE;
     for (int e = tid; e < NE; e += NT) {
       em[e] = pem[e];
-      cqd[e] = (double)pw[e];
+      if constexpr (MASSES) cqd[e] = (double)pw[e];
     }
     for (int s = tid; s < p.n_slices; s += NT) bad |= p.pre_st[(int64_t)row * p.n_slices + s];
     __syncthreads();  // status cleared before any thread sets a bit
@@ -1092,7 +1099,8 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
-        for (int e = tid; e < NE; e += NT) cq[e] = 0;
+        if constexpr (MASSES)
+          for (int e = tid; e < NE; e += NT) cq[e] = 0;
         __syncthreads();
         if (p.has_pen) U = build_history<NT, HR, SLICE>(p, row, hi, h, m);
         landed(hi);  // the ids are read under conditions; end their loads on every path
@@ -1109,13 +1117,14 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
             if ((t + 1) * TILE <= p.V) make_z<G, false>(x, base, p, h.bitmap, z, bad);
             else make_z<G, true>(x, base, p, h.bitmap, z, bad);
             float mc;
-            double rs4;
-            span_stats<G>(z, lane, mc, rs4);
+            double rs4 = 0.0;
+            span_stats<G, MASSES>(z, lane, mc, rs4);
             // the lane's 256-id chunk: the span, or its half for G = 8
             const int e = (t * TILE + wid * 64 * G) / MASS_CHUNK + (G == 4 ? 0 : (lane >> 5));
             if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) em[e] = mc;
             // rows 0 + 1 (and 2 + 3) are one chunk: each row's lane 0 adds its total
-            if ((lane & 15) == 0 && e < NE) atomicAdd(&cqd[e], rs4);
+            if constexpr (MASSES)
+              if ((lane & 15) == 0 && e < NE) atomicAdd(&cqd[e], rs4);
           }
         }
         for (int i = tid; i < n; i += NT) {
@@ -1154,7 +1163,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     double Sg;
     combine_states(p.sh_states, p.n_shards, p.nrows, row, Mref, Sg);
   }
-  if constexpr (DRAW != DRAW_SHARD_RACE) {  // the race over slices takes the gathered states
+  if constexpr (DRAW != DRAW_SHARD_RACE && MASSES) {  // the race over slices takes the gathered states
     for (int c = tid; c < NE; c += NT) {
       uint64_t q = scale_mass((uint64_t)cqd[c], mass_ff(em[c], Mref));
       if (p.has_pen) {
@@ -1346,7 +1355,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     }
     return;
   }
-  if (wid == 0) {
+  if (MASSES && wid == 0) {
     uint64_t own, qincl;
     const uint64_t S = mass_scan(own, qincl);  // the log-prob's total
     if constexpr (PLACES) {
@@ -1492,7 +1501,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
         // and the finish flags the row.
         p.sh_out_picks[row] = dsv41_full_pick{m->bi[0] >= 0 ? tok + p.voff : -1, ztok, 0.0f};
       } else {
-        write_result(p, row, m, tok, row_lp(ztok, S), p.V);
+        write_result(p, row, m, tok, MASSES ? row_lp(ztok, S) : __builtin_nanf(""), p.V);
       }
     }
   }
@@ -3136,11 +3145,11 @@ __global__ __launch_bounds__(256) void full_finish_kernel(dsv41_sampler_full_fin
   }
   if (st & (ST_NONFINITE | ST_BAD_SLICES)) {
     d.out_ids[row] = -1;
-    d.out_logprob[row] = __builtin_nanf("");
+    if (d.out_logprob) d.out_logprob[row] = __builtin_nanf("");
     if (d.out_kept) d.out_kept[row] = 0;
   } else {
     d.out_ids[row] = tok;
-    d.out_logprob[row] = (float)(((double)ztok - (double)M) - log(S));
+    if (d.out_logprob) d.out_logprob[row] = (float)(((double)ztok - (double)M) - log(S));
     if (d.out_kept) d.out_kept[row] = (int32_t)d.vocab_size;
   }
   d.out_status[row] = st;
@@ -3203,8 +3212,8 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   if (!(d->min_p >= 0.0f && d->min_p <= 1.0f)) return fail(DSV41_E_INVALID, "min_p must be in [0, 1]");
   if (!shard && !d->greedy && !d->uniforms && !d->replay_ids)
     return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
-  if (!shard && (!d->out_ids || !d->out_logprob || !d->out_status))
-    return fail(DSV41_E_INVALID, "out_ids, out_logprob and out_status are required");
+  if (!shard && (!d->out_ids || !d->out_status)) return fail(DSV41_E_INVALID, "out_ids and out_status are required");
+  if (!shard && d->replay_ids && !d->out_logprob) return fail(DSV41_E_INVALID, "replay_ids need out_logprob");
   const bool pen_on = d->repetition_penalty != 1.0f || d->presence_penalty != 0.0f || d->frequency_penalty != 0.0f;
   const bool hist_given = d->history != nullptr && (d->history_lens != nullptr || d->hist_len > 0);
   if (hist_given) {
@@ -3495,24 +3504,38 @@ static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params
 // A small FULL batch: the slices' statistics, then one finishing workgroup per row.
 static int run_presliced(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, hipStream_t s) {
   const dim3 grid(d->rows * pl.pre_slices), block(PRE_NT);
-  const bool bf = pl.esize == 2, ex = !p.greedy;
+  const bool bf = pl.esize == 2, ex = !p.greedy, lp = p.out_lp != nullptr;
   // no dynamic LDS (a little static LDS for the block vote): no attribute to raise
   if (bf) {
-    if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false>), grid, block, 0, s, p);
+    if (lp) {
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false>), grid, block, 0, s, p);
+    } else {
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, false>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, false>), grid, block, 0, s, p);
+    }
   } else {
-    if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((full_slice_kernel<float, 4, false>), grid, block, 0, s, p);
+    if (lp) {
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false>), grid, block, 0, s, p);
+    } else {
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true, false>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false, false>), grid, block, 0, s, p);
+    }
   }
   DSV41_HIP_CHECK(hipGetLastError());
   if (bf) {
     if (ex) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s)
                           : launch(full_kernel<uint16_t, 8, false, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s);
+    if (!lp) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_ARGMAX, true>, FULL_NT, pl.lds, d->rows, p, s)
+                           : launch(full_kernel<uint16_t, 8, false, DRAW_ARGMAX, true>, FULL_NT, pl.lds, d->rows, p, s);
     return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s)
                   : launch(full_kernel<uint16_t, 8, false, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s);
   }
   if (ex) return pl.vec ? launch(full_kernel<float, 4, true, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s)
                         : launch(full_kernel<float, 4, false, DRAW_CDF, true>, FULL_NT, pl.lds, d->rows, p, s);
+  if (!lp) return pl.vec ? launch(full_kernel<float, 4, true, DRAW_ARGMAX, true>, FULL_NT, pl.lds, d->rows, p, s)
+                         : launch(full_kernel<float, 4, false, DRAW_ARGMAX, true>, FULL_NT, pl.lds, d->rows, p, s);
   return pl.vec ? launch(full_kernel<float, 4, true, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s)
                 : launch(full_kernel<float, 4, false, DRAW_GREEDY, true>, FULL_NT, pl.lds, d->rows, p, s);
 }
@@ -3531,6 +3554,12 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
                               : launch(full_kernel<uint16_t, 8, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
         return pl.vec ? launch(full_kernel<float, 4, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
                       : launch(full_kernel<float, 4, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
+      }
+      if (p.greedy && !p.out_lp) {
+        if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_ARGMAX>, FULL_NT, pl.lds, d->rows, p, s)
+                              : launch(full_kernel<uint16_t, 8, false, DRAW_ARGMAX>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_ARGMAX>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 4, false, DRAW_ARGMAX>, FULL_NT, pl.lds, d->rows, p, s);
       }
       if (p.greedy) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s)
@@ -3692,8 +3721,8 @@ extern "C" int dsv41_sampler_merge_run(const dsv41_sampler_merge_desc* d, void* 
   if (!(d->top_p > 0.0f && d->top_p <= 1.0f)) return fail(DSV41_E_INVALID, "top_p must be in (0, 1]");
   if (!(d->min_p >= 0.0f && d->min_p <= 1.0f)) return fail(DSV41_E_INVALID, "min_p must be in [0, 1]");
   if (!d->greedy && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
-  if (!d->keys || !d->counts || !d->status || !d->out_ids || !d->out_logprob || !d->out_status)
-    return fail(DSV41_E_INVALID, "sampler merge: keys, counts, status, out_ids, out_logprob and out_status are required");
+  if (!d->keys || !d->counts || !d->status || !d->out_ids || !d->out_status)
+    return fail(DSV41_E_INVALID, "sampler merge: keys, counts, status, out_ids and out_status are required");
   const int64_t cap = (int64_t)d->n_shards * std::min<int64_t>(d->max_candidates, d->top_k);
   const size_t lds = merge_lds_bytes((size_t)cap, d->top_k);
   if (lds > LDS_LIMIT) return fail(DSV41_E_UNSUPPORTED, "sampler merge: n_shards * top_k exceeds the on-chip candidate buffer");
@@ -3812,8 +3841,7 @@ extern "C" int dsv41_sampler_full_finish_run(const dsv41_sampler_full_finish_des
   if (!d->states || (d->draw != DSV41_FULL_DRAW_GREEDY && !d->picks))
     return fail(DSV41_E_INVALID, "sampler full finish: states (and picks, unless greedy) are required");
   if (d->draw == DSV41_FULL_DRAW_CDF && !d->uniforms) return fail(DSV41_E_INVALID, "sampling requires one uniform per row");
-  if (!d->out_ids || !d->out_logprob || !d->out_status)
-    return fail(DSV41_E_INVALID, "out_ids, out_logprob and out_status are required");
+  if (!d->out_ids || !d->out_status) return fail(DSV41_E_INVALID, "out_ids and out_status are required");
   hipLaunchKernelGGL(full_finish_kernel, dim3((d->rows + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
                      *d);
   DSV41_HIP_CHECK(hipGetLastError());

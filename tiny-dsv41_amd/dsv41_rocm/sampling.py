@@ -31,10 +31,11 @@ from . import _lib
 @dataclass
 class SampleResult:
     """Per-row outputs: drawn ids (int64), their log-probs under the processed
-    distribution (fp32), kept-set sizes (int32) and status bits (int32)."""
+    distribution (fp32; None when not requested), kept-set sizes (int32) and status bits
+    (int32)."""
 
     ids: torch.Tensor
-    logprobs: torch.Tensor
+    logprobs: Optional[torch.Tensor]
     kept: torch.Tensor
     status: torch.Tensor
 
@@ -146,6 +147,7 @@ def sample(
     greedy: bool = False,
     check: bool = True,
     exponentials: Optional[torch.Tensor] = None,
+    logprobs: bool = True,
 ) -> SampleResult:
     """Sample one token per row of ``logits[rows, vocab]`` (fp32 or bf16, on the GPU).
 
@@ -166,6 +168,10 @@ def sample(
     the CPU; fed the variates of ``torch.empty(V).exponential_(1, generator=g)`` it returns
     the reference's token (rollout.py:147-148) and leaves ``g`` where the reference leaves it.
     Only without top-k / top-p / min-p.
+
+    ``logprobs=False`` leaves the log-probs out (``SampleResult.logprobs`` is None); a greedy
+    draw without truncation then forms no masses at all, only each row's first maximum
+    (the reference's greedy, ``sft_eval.py:64``, is an argmax).
     """
     logits, history, history_lens = _rows_in(logits, history, history_lens, temperature, top_k)
     rows, vocab = logits.shape
@@ -186,7 +192,7 @@ def sample(
         if uniforms.shape != (rows,):
             raise ValueError("one uniform is required per row")
     ids = torch.empty(rows, dtype=torch.int64, device=device)
-    lps = torch.empty(rows, dtype=torch.float32, device=device)
+    lps = torch.empty(rows, dtype=torch.float32, device=device) if logprobs else None
     kept = torch.empty(rows, dtype=torch.int32, device=device)
     status = torch.empty(rows, dtype=torch.int32, device=device)
     desc = _rows_desc(logits, history, history_lens, temperature, repetition_penalty, presence_penalty,
@@ -196,7 +202,7 @@ def sample(
     desc.uniforms = _device_ptr(uniforms)
     desc.greedy = 1 if greedy else 0
     desc.out_ids = ids.data_ptr()
-    desc.out_logprob = lps.data_ptr()
+    desc.out_logprob = _device_ptr(lps)
     desc.out_kept = kept.data_ptr()
     desc.out_status = status.data_ptr()
     if exponentials is not None and not greedy:
