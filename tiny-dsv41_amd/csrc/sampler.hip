@@ -1174,7 +1174,7 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
     }
     __syncthreads();
   }
-  // S in wave 0: lane l sums the contiguous run of chunks [b, e), then a wave scan (every
+  // S in wave 0: lane l sums the contiguous run of chunks [rb, re), then a wave scan (every
   // lane returns S, `own` its run and `incl` the run's inclusive prefix)
   const int run = (NE + 63) / 64;
   const int rb = min(lane * run, NE), re = min(rb + run, NE);
