@@ -69,14 +69,16 @@ def test_log_prob_is_against_the_exact_mass_total(draw):
         assert lps[r] == want, (r, lps[r], want)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("vocab", [1, 255, 256, 257, 151936, 2097151])
-def test_log_prob_total_closed_forms(vocab):
+def test_log_prob_total_closed_forms(vocab, dtype):
     """The exact total in closed form.  Equal logits: every id weighs 2^43, so S = V 2^43 and
     every draw reports lp = -log V.  Two levels (k ids at 0, the rest at -d): an all-low chunk
     weighs its count times g = floor(2^43 exp32(-d)) exactly, and a mixed chunk holds its
     masses unscaled, so S = k 2^43 + (V - k) g whatever the chunking, and the drawn id reports
     z_tok - log(S 2^-43).  Ids at -60 weigh nothing.  The floats must be those of numpy's fp64
-    log, bit for bit, for the inverse CDF, the race, greedy and the replay."""
+    log, bit for bit, for the inverse CDF, the race, greedy and the replay, on fp32 and bf16
+    rows (the three values are exact in both)."""
     g = torch.Generator().manual_seed(vocab)
     rows = 3
     x = torch.zeros(rows, vocab)
@@ -86,10 +88,10 @@ def test_log_prob_total_closed_forms(vocab):
     x[1, top] = 0.0
     x[2] = -60.0  # below the 2^-43 resolution: the low ids weigh nothing
     x[2, top] = 0.0
-    print(f"case: vocab {vocab} top ids {k}", flush=True)
+    print(f"case: vocab {vocab} top ids {k} dtype {dtype}", flush=True)
     gm = oracle.mass(-7.25, 0.0)
     totals = [vocab << 43, (k << 43) + (vocab - k) * gm, k << 43]  # S per row, exact integers
-    xd = x.to(DEV)
+    xd = x.to(dtype).to(DEV)
     draws = {
         "cdf": sample(xd, uniforms=torch.rand(rows, generator=g).to(DEV)),
         "race": sample(xd, exponentials=torch.empty(rows, vocab).exponential_(1, generator=g).to(DEV)),
