@@ -724,40 +724,55 @@ __device__ __forceinline__ void make_z(const float (&x)[G], int base, const Para
                                        const uint32_t* bitmap, float (&z)[G], int& bad) {
   uint32_t pen = 0;
   if (p.has_pen && (!TAIL || base < p.V)) pen = (bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u);
-  // 2^-100 <= |x| < 2^100: the three-operation division is IEEE-exact there (checked
-  // exhaustively on the host); outside it, IEEE division.
-  uint32_t lo = 0xFFFFFFFFu, hi = 0;
+  // a non-finite logit outside the history and inside the row flags the row (history ids are
+  // checked where their penalized value is formed; ids past the row read 0)
+  auto check = [&](const float (&v)[G]) {
 #pragma unroll
-  for (int j = 0; j < G; ++j) {
-    const uint32_t a = __float_as_uint(x[j]) & 0x7FFFFFFFu;
-    lo = min(lo, a);
-    hi = max(hi, a);
-  }
-  const bool fast = p.fast_div && lo >= 0x0D800000u && hi < 0x71800000u;
-  if (fast) {
-    if (p.unit_T) {
+    for (int j = 0; j < G; ++j)
+      if ((!TAIL || base + j < p.V) && !((pen >> j) & 1u) && !isfinite(v[j])) bad = 1;
+  };
+  if (p.unit_T) {
+    // x / 1 = x for every x: one class test per logit, the exact check only when one fails
+    bool nf = false;
 #pragma unroll
-      for (int j = 0; j < G; ++j) z[j] = x[j];
-    } else {
+    for (int j = 0; j < G; ++j) {
+      z[j] = x[j];
+      nf |= __builtin_amdgcn_classf(x[j], 0x207);  // NaN or an infinity
+    }
+    if (nf) check(z);
+  } else {
+    // 2^-100 <= |x| < 2^100: the three-operation division is IEEE-exact there (checked
+    // exhaustively on the host); outside it, IEEE division.
+    uint32_t lo = 0xFFFFFFFFu, hi = 0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const uint32_t a = __float_as_uint(x[j]) & 0x7FFFFFFFu;
+      lo = min(lo, a);
+      hi = max(hi, a);
+    }
+    if (p.fast_div && lo >= 0x0D800000u && hi < 0x71800000u) {
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         const float q = x[j] * p.rT;
         const float e = __builtin_fmaf(-q, p.T, x[j]);
         z[j] = __builtin_fmaf(e, p.rT, q);
       }
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-      z[j] = x[j] / p.T;
-      if ((!TAIL || base + j < p.V) && !((pen >> j) & 1u) && !isfinite(z[j])) bad = 1;
+      for (int j = 0; j < G; ++j) z[j] = x[j] / p.T;
+      check(z);
     }
   }
   if (p.has_pen) {
+    // history ids read -inf here: a signed one-bit field gives an all-ones or zero mask and
+    // v_bfi_b32 picks by it (a compare and v_cndmask through VCC would cost wait states)
+    const uint32_t ninf = NEG_INF_BITS;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      const uint32_t msk = 0u - ((pen >> j) & 1u);
-      z[j] = __uint_as_float((msk & NEG_INF_BITS) | (~msk & __float_as_uint(z[j])));
+      const uint32_t msk = (uint32_t)__builtin_amdgcn_sbfe((int)pen, j, 1);
+      uint32_t r;
+      asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(msk), "s"(ninf), "v"(__float_as_uint(z[j])));
+      z[j] = __uint_as_float(r);
     }
   }
   if (TAIL) {
