@@ -61,7 +61,9 @@ __device__ __forceinline__ int wave_min_i(int v) {
 // then combined from readlanes, so the returned value is identical in every lane.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+  // quad_perm and row_ror only: every lane reads a lane of its own row, so no old value is
+  // needed (bound_ctrl), and the move can fold into the instruction that uses it
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float rl(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
