@@ -563,7 +563,7 @@ def test_nonfinite_history_tokens_and_penalty_overflow():
     """NaN, +inf and -inf on history tokens, a -inf elsewhere, and a finite logit that
     only overflows once the repetition penalty multiplies it, under lowering penalties
     (history met in the stream, with and without counts) and under raising ones
-    (history gathered)."""
+    (history gathered), with top-k and without truncation."""
     g = torch.Generator().manual_seed(9)
     rows, V = 6, 9000
     logits = torch.randn(rows, V, generator=g)
@@ -577,7 +577,12 @@ def test_nonfinite_history_tokens_and_penalty_overflow():
     u = torch.rand(rows, generator=g)
     for knobs in (dict(repetition_penalty=1.5, top_k=20),
                   dict(repetition_penalty=1.5, frequency_penalty=0.2, top_k=20, min_p=0.1),
-                  dict(repetition_penalty=0.7, presence_penalty=-0.2, top_k=20)):
+                  dict(repetition_penalty=0.7, presence_penalty=-0.2, top_k=20),
+                  # no truncation: the full-vocabulary kernel, at temperature 1 (one class
+                  # test per logit) and otherwise (the division's range guard)
+                  dict(repetition_penalty=1.5),
+                  dict(presence_penalty=0.5, frequency_penalty=0.2),
+                  dict(repetition_penalty=1.5, temperature=0.7)):
         gpu, ora = run_both(logits, u, hist, **knobs)
         np.testing.assert_array_equal(gpu[3], ora[3])
         assert all(gpu[3][r] & 1 for r in (0, 1, 2, 4)) and not gpu[3][5] & 1
