@@ -678,6 +678,15 @@ __device__ __forceinline__ void load_group(Raw<TIn, G>& r, __amdgpu_buffer_rsrc_
     r.w[1] = (uint32_t)v.y;
     r.w[2] = (uint32_t)v.z;
     r.w[3] = (uint32_t)v.w;
+  } else if constexpr (VEC && WORDS == 8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * h, 0, CPOL);
+      r.w[4 * h] = (uint32_t)v.x;
+      r.w[4 * h + 1] = (uint32_t)v.y;
+      r.w[4 * h + 2] = (uint32_t)v.z;
+      r.w[4 * h + 3] = (uint32_t)v.w;
+    }
   } else if constexpr (VEC && WORDS == 2) {
     const v2i v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, CPOL);
     r.w[0] = (uint32_t)v.x;
@@ -852,7 +861,8 @@ __device__ __forceinline__ void landed(const HistIds<HR, IdT>& hi) {
 // LOWERING: the caller meets history tokens in the stream itself when p.pen_lowers is
 // set, and the gather is off then (a compile-time switch: an extra runtime flag costs
 // full_kernel the scalar registers that keep it at two workgroups per CU).
-template <typename TIn, int G, int NT, bool VEC, bool LOWERING, int CPOL = STREAM_CPOL, class Setup, class Batch>
+template <typename TIn, int G, int NT, bool VEC, bool LOWERING, int CPOL = STREAM_CPOL, int PF = dsv41::sampler::PF,
+          class Setup, class Batch>
 __device__ __forceinline__ void stream_row(const Params& p, __amdgpu_buffer_rsrc_t rs, const Hist& h,
                                            Setup setup, Batch batch) {
   constexpr int TILE = NT * G;
@@ -1060,8 +1070,14 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
 // ====================================================================== FULL
 // No truncation: kept set = whole vocabulary.  Span c = [c*64G, (c+1)*64G) is one wave's
 // span of one tile; the exact masses of its one or two 256-id chunks go to LDS.
+// fp32 rows of the draws that form masses take 8 logits per lane (two 16-byte loads) in
+// batches of 2 tiles: the bytes in flight of 4 tiles of 4, and each wave span's reductions
+// spread over 8 logits.  The massless argmax and the spread small batches keep 4 per lane,
+// whose loads read whole contiguous kilobytes (measured faster there).
+template <typename TIn, int G>
+constexpr int full_pf() { return sizeof(TIn) * G > 16 ? 2 : PF; }
 template <typename TIn, int G, bool VEC, int DRAW, bool PRE = false>
-__global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p) {
+__global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
   extern __shared__ __align__(16) unsigned char smem[];
   const Layout L = make_layout<MODE_FULL, G>(p.V, p.words, p.ucap, 0);
@@ -1110,7 +1126,8 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
   } else {
   HistIds<HR> hi;
   load_history<NT, HR>(p, row, hi);
-  stream_row<TIn, G, NT, VEC, false, FULL_CPOL>(
+  constexpr int FPF = full_pf<TIn, G>();
+  stream_row<TIn, G, NT, VEC, false, FULL_CPOL, FPF>(
       p, rs, h,
       [&]() {
         if (tid == 0) m->status = 0;
@@ -1121,9 +1138,9 @@ __global__ __launch_bounds__(FULL_NT, G == 4 ? 8 : 1) void full_kernel(Params p)
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
-      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+      [&](int t0, int nt, Raw<TIn, G>(&R)[FPF], int s0, int n, float gx) {
 #pragma unroll
-        for (int k = 0; k < PF; ++k) {
+        for (int k = 0; k < FPF; ++k) {
           const int t = t0 + k;
           if (t < nt) {
             const int base = t * TILE + tid * G;
@@ -3277,8 +3294,7 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   pl->cap = pl->mode == MODE_TOPK ? k_eff + TOPK_TILE : pl->mode == MODE_TOPP ? TOPP_CAP : 0;
   Layout L;
   if (pl->mode == MODE_FULL)
-    L = pl->esize == 4 ? make_layout<MODE_FULL, 4>(V, pl->words, pl->ucap, 0)
-                       : make_layout<MODE_FULL, 8>(V, pl->words, pl->ucap, 0);
+    L = make_layout<MODE_FULL, 8>(V, pl->words, pl->ucap, 0);  // the same for 4 or 8 logits per lane
   else if (pl->mode == MODE_TOPK)
     L = make_layout<MODE_TOPK, TOPK_G>(V, pl->words, pl->ucap, pl->cap);
   else if (pl->mode == MODE_TOPP)
@@ -3346,7 +3362,7 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   pl->pre_slices = 0;
   if (!shard && pl->mode == MODE_FULL && !pl->has_pen && !d->replay_ids && !d->exponentials &&
       d->rows <= PRE_MAX_ROWS) {
-    const int G = pl->esize == 4 ? 4 : 8;
+    const int G = pl->esize == 4 ? 4 : 8;  // the spread small batches take 4 fp32 logits per lane
     const int NC = (V + 64 * G - 1) / (64 * G), NE = n_mass_chunks(V);
     const int want = std::max(2, 512 / d->rows);
     const int sw = std::max(PRE_NT / 64, (NC + want - 1) / want);  // at least one span per wave
@@ -3567,8 +3583,8 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
       if (p.replay) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
                               : launch(full_kernel<uint16_t, 8, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
-        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
-                      : launch(full_kernel<float, 4, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 8, true, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 8, false, DRAW_REPLAY>, FULL_NT, pl.lds, d->rows, p, s);
       }
       if (p.greedy && !p.out_lp) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_ARGMAX>, FULL_NT, pl.lds, d->rows, p, s)
@@ -3579,19 +3595,19 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
       if (p.greedy) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s)
                               : launch(full_kernel<uint16_t, 8, false, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s);
-        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s)
-                      : launch(full_kernel<float, 4, false, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 8, true, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 8, false, DRAW_GREEDY>, FULL_NT, pl.lds, d->rows, p, s);
       }
       if (p.exps) {
         if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s)
                               : launch(full_kernel<uint16_t, 8, false, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s);
-        return pl.vec ? launch(full_kernel<float, 4, true, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s)
-                      : launch(full_kernel<float, 4, false, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s);
+        return pl.vec ? launch(full_kernel<float, 8, true, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s)
+                      : launch(full_kernel<float, 8, false, DRAW_RACE>, FULL_NT, pl.lds, d->rows, p, s);
       }
       if (bf) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
                             : launch(full_kernel<uint16_t, 8, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
-      return pl.vec ? launch(full_kernel<float, 4, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
-                    : launch(full_kernel<float, 4, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
+      return pl.vec ? launch(full_kernel<float, 8, true, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s)
+                    : launch(full_kernel<float, 8, false, DRAW_CDF>, FULL_NT, pl.lds, d->rows, p, s);
     case MODE_TOPK: {
       if (pl.slices > 1) return run_sliced(d, pl, p, static_cast<char*>(workspace), s);
       if (pl.topk_nt == 256) {
@@ -3815,8 +3831,8 @@ template <int DRAW>
 static int launch_full(const Plan& pl, int rows, const Params& p, hipStream_t s) {
   if (pl.esize == 2) return pl.vec ? launch(full_kernel<uint16_t, 8, true, DRAW>, FULL_NT, pl.lds, rows, p, s)
                                    : launch(full_kernel<uint16_t, 8, false, DRAW>, FULL_NT, pl.lds, rows, p, s);
-  return pl.vec ? launch(full_kernel<float, 4, true, DRAW>, FULL_NT, pl.lds, rows, p, s)
-                : launch(full_kernel<float, 4, false, DRAW>, FULL_NT, pl.lds, rows, p, s);
+  return pl.vec ? launch(full_kernel<float, 8, true, DRAW>, FULL_NT, pl.lds, rows, p, s)
+                : launch(full_kernel<float, 8, false, DRAW>, FULL_NT, pl.lds, rows, p, s);
 }
 
 extern "C" int dsv41_sampler_full_state_run(const dsv41_sampler_full_shard_desc* d, void* stream) {
