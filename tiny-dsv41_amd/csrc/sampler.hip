@@ -1071,11 +1071,12 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
 // No truncation: kept set = whole vocabulary.  Span c = [c*64G, (c+1)*64G) is one wave's
 // span of one tile; the exact masses of its one or two 256-id chunks go to LDS.
 // fp32 rows of the draws that form masses take 8 logits per lane (two 16-byte loads) in
-// batches of 2 tiles: the bytes in flight of 4 tiles of 4, and each wave span's reductions
-// spread over 8 logits.  The massless argmax and the spread small batches keep 4 per lane,
+// batches of one tile, so that each wave span's reductions spread over 8 logits; the two
+// tiles in flight (128 KiB per CU at two workgroups) cover the latency of this ALU-bound
+// stream.  The massless argmax and the spread small batches keep 4 per lane,
 // whose loads read whole contiguous kilobytes (measured faster there).
 template <typename TIn, int G>
-constexpr int full_pf() { return sizeof(TIn) * G > 16 ? 2 : PF; }
+constexpr int full_pf() { return sizeof(TIn) * G > 16 ? 1 : PF; }
 template <typename TIn, int G, bool VEC, int DRAW, bool PRE = false>
 __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel(Params p) {
   constexpr int NT = FULL_NT, NW = NT / 64, HR = 4;
