@@ -56,24 +56,52 @@ __device__ __forceinline__ int wave_min_i(int v) {
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
   return v;
 }
-// DPP reductions (all 64 lanes must be active).  Within each 16-lane row: swap
-// neighbours, swap pairs (quad_perm), rotate by 4 and by 8; the four row results are
-// then combined from readlanes, so the returned value is identical in every lane.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  // quad_perm and row_ror only: every lane reads a lane of its own row, so no old value is
-  // needed (bound_ctrl), and the move can fold into the instruction that uses it
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+// Maxima of quiet operands (all 64 lanes active).  In IEEE mode the compiler's fmaxf first
+// turns a signaling NaN into a quiet one, a v_max per operand that also keeps the DPP move
+// from folding into the max.  For operands that are not signaling NaNs (fmaxf and arithmetic
+// results, or values passed through __builtin_canonicalizef) a plain v_max_f32 returns
+// fmaxf's value, and maxima of such values are quiet again.  A DPP or permlane read of a
+// register that the instruction before wrote needs two wait states (s_nop 1).  Each block
+// ends with one too: the compiler does not count the asm as the VALU write that a later
+// DPP read of its result must wait for.
+//   row_max_q: every lane gets its 16-lane row's maximum (quad_perm swaps, row_ror 4, 8);
+//   pair_max_q: rows 0, 1 and rows 2, 3 combined (v_permlane16_swap), so every lane of
+//     lanes 0-31 holds their maximum and every lane of 32-63 theirs;
+//   halves_max_q: the two 32-lane halves combined (v_permlane32_swap).
+__device__ __forceinline__ float row_max_q(float v) {
+  asm("s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1"
+      : "+v"(v));
+  return v;
 }
-__device__ __forceinline__ float rl(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+__device__ __forceinline__ float pair_max_q(float v) {
+  float w = v;
+  asm("s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "v_max_f32 %0, %0, %1\n\t"
+      "s_nop 1"
+      : "+v"(v), "+v"(w));
+  return v;
 }
+__device__ __forceinline__ float halves_max_q(float v) {
+  float w = v;
+  asm("s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "v_max_f32 %0, %0, %1\n\t"
+      "s_nop 1"
+      : "+v"(v), "+v"(w));
+  return v;
+}
+// fmaxf over the 64 lanes, the same value in every lane
 __device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_f32<0x124>(v));  // row_ror:4
-  v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
-  return fmaxf(fmaxf(rl(v, 0), rl(v, 16)), fmaxf(rl(v, 32), rl(v, 48)));
+  return halves_max_q(pair_max_q(row_max_q(__builtin_canonicalizef(v))));
 }
 
 // inclusive prefix sums across the 64 lanes (all lanes active).  Integer sums are exact in

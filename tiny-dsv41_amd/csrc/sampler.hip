@@ -276,15 +276,17 @@ __device__ __forceinline__ float mass_ff(float z, float zmax) {
   const float n = __builtin_rintf(d * 0x1.715476p+0f);
   float r = __builtin_fmaf(-n, 0x1.62e4p-1f, d);
   r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
-  float p = 0x1.a01a02p-13f;
-  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
-  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
-  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
-  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  return __builtin_floorf(__builtin_ldexpf(p, (int)n + 43));
+  // The coefficients carry the 2^43: every Horner value is 2^43 times the unscaled one,
+  // rounding included (all values stay normal), so only the 2^n scale remains.
+  float p = 0x1.a01a02p+30f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p+33f);
+  p = __builtin_fmaf(p, r, 0x1.111112p+36f);
+  p = __builtin_fmaf(p, r, 0x1.555556p+38f);
+  p = __builtin_fmaf(p, r, 0x1.555556p+40f);
+  p = __builtin_fmaf(p, r, 0x1p+42f);
+  p = __builtin_fmaf(p, r, 0x1p+43f);
+  p = __builtin_fmaf(p, r, 0x1p+43f);
+  return __builtin_floorf(__builtin_ldexpf(p, (int)n));
 }
 
 __device__ __forceinline__ uint64_t mass_of(float z, float zmax) { return (uint64_t)mass_ff(z, zmax); }
@@ -958,17 +960,6 @@ __device__ __forceinline__ Hist hist_tables(unsigned char* smem, const Layout& L
   return h;
 }
 
-// Row (16-lane) maxima of v, the same value in every lane: r[k] over lanes 16k .. 16k+15.
-__device__ __forceinline__ void row_max4(float v, float (&r)[4]) {
-  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_f32<0x124>(v));  // row_ror:4
-  v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
-  r[0] = rl(v, 0);
-  r[1] = rl(v, 16);
-  r[2] = rl(v, 32);
-  r[3] = rl(v, 48);
-}
 // Each lane's 16-lane row total of v (fp64, by the same DPP steps).
 template <int CTRL>
 __device__ __forceinline__ double dpp_f64(double v) {
@@ -996,17 +987,17 @@ __device__ __forceinline__ uint64_t scale_mass(uint64_t w, float g) {
 // order (a chunk's total is below 2^51).
 template <int G, bool MASSES = true>
 __device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float& mc, double& rs4) {
+  static_assert(G == 4 || G == 8, "a mass chunk is the span (G 4) or its half (G 8)");
+  (void)lane;
   float mx = z[0];
 #pragma unroll
   for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
-  float rmx[4];
-  row_max4(mx, rmx);
-  mc = G == 4 ? fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]))
-              : (lane < 32 ? fmaxf(rmx[0], rmx[1]) : fmaxf(rmx[2], rmx[3]));
+  mx = pair_max_q(row_max_q(__builtin_canonicalizef(mx)));
+  mc = G == 4 ? halves_max_q(mx) : mx;
   if constexpr (MASSES) {
-    double qd = 0.0;
+    double qd = (double)mass_ff(z[0], mc);
 #pragma unroll
-    for (int j = 0; j < G; ++j) qd += (double)mass_ff(z[j], mc);
+    for (int j = 1; j < G; ++j) qd += (double)mass_ff(z[j], mc);
     rs4 = row_sum_f64(qd);
   }
 }
