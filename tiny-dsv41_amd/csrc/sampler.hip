@@ -349,7 +349,7 @@ template <int NT>
 __device__ __forceinline__ float block_max(float v, Misc* m) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  v = wave_max(v);
+  v = wave_max_dpp(v);
   if (lane == 0) m->rf[wid] = v;
   __syncthreads();
   float r = m->rf[0];
@@ -1002,6 +1002,11 @@ __device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float&
   }
 }
 
+__device__ __forceinline__ uint64_t rl_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ double rl_d(double v, int lane) {
   const uint64_t b = (uint64_t)__double_as_longlong(v);
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
@@ -1104,6 +1109,12 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
   constexpr int TILE = NT * G;
   int bad = 0;
   int U = 0;
+  // This thread's running maximum of chunk maxima and history z.  bf16 rows (one workgroup
+  // per CU, whose serial phases nothing hides) keep it during the stream; fp32 rows run at
+  // the 64-register cap, where one more live register costs the stream more than reading
+  // the tables afterwards does.
+  constexpr bool RUN_MAX = PRE || sizeof(TIn) == 2;
+  float lmax = NEG_INF;
   if constexpr (PRE) {
     // the span statistics full_slice_kernel formed (no penalties on this path)
     if (tid == 0) m->status = 0;
@@ -1111,6 +1122,7 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
     const uint64_t* pw = p.pre_w + (int64_t)row * NE;
     for (int e = tid; e < NE; e += NT) {
       em[e] = pem[e];
+      lmax = fmaxf(lmax, em[e]);
       if constexpr (MASSES) cqd[e] = (double)pw[e];
     }
     for (int s = tid; s < p.n_slices; s += NT) bad |= p.pre_st[(int64_t)row * p.n_slices + s];
@@ -1143,6 +1155,7 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
             float mc;
             double rs4 = 0.0;
             span_stats<G, MASSES>(z, lane, mc, rs4);
+            if constexpr (RUN_MAX) lmax = fmaxf(lmax, mc);
             // the lane's 256-id chunk: the span, or its half for G = 8
             const int e = (t * TILE + wid * 64 * G) / MASS_CHUNK + (G == 4 ? 0 : (lane >> 5));
             if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) em[e] = mc;
@@ -1157,17 +1170,19 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
           const float z = pen_z(x, count_of(h, s), p);
           if (!isfinite(z)) bad = 1;
           penz[s] = z;
+          if constexpr (RUN_MAX) lmax = fmaxf(lmax, z);
         }
       });
   }
   if (bad) atomicOr(&m->status, ST_NONFINITE);
-  __syncthreads();
-
-  float pmax = NEG_INF;
-  for (int s = tid; s < U; s += NT) pmax = fmaxf(pmax, penz[s]);
-  float cmax = NEG_INF;
-  for (int c = tid; c < NE; c += NT) cmax = fmaxf(cmax, em[c]);
-  const float M = block_max<NT>(fmaxf(pmax, cmax), m);
+  if constexpr (!RUN_MAX) {
+    __syncthreads();
+    for (int s = tid; s < U; s += NT) lmax = fmaxf(lmax, penz[s]);
+    for (int c = tid; c < NE; c += NT) lmax = fmaxf(lmax, em[c]);
+  }
+  // the row maximum over the chunk maxima and the history tokens' z (the barriers inside
+  // also publish the stream's LDS tables)
+  const float M = block_max<NT>(lmax, m);
 
   // The draws use 2^-43 fixed-point masses, exact integers, so neither the drawn id nor
   // the reported log-prob depends on the order of any reduction.  The row (or slice) is cut
@@ -1187,50 +1202,93 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
     double Sg;
     combine_states(p.sh_states, p.n_shards, p.nrows, row, Mref, Sg);
   }
+  // The inverse-CDF draws need the uniform before the masses are scanned; a slice of a
+  // sharded draw learns here whether its masses hold the target at all.
+  const float u = PLACES ? row_uniform(p, row, m) : 0.0f;
+  uint64_t tq = 0;  // the draw's target in this workgroup's masses
+  if constexpr (DRAW == DRAW_SHARD_CDF) {
+    // Every slice finds, from the same gathered masses, the slice whose masses hold the
+    // target; only that one places the token, against the target less the masses before it.
+    uint64_t Sall = 0;
+    for (int s = 0; s < p.n_shards; ++s) Sall += p.sh_masses[(int64_t)s * p.nrows + row];
+    const uint64_t t = draw_target(u, Sall);
+    uint64_t acc = 0;
+    int owner = -1;
+    for (int s = 0; s < p.n_shards; ++s) {
+      const uint64_t q = p.sh_masses[(int64_t)s * p.nrows + row];
+      if (owner < 0 && t < acc + q) {
+        owner = s;
+        tq = t - acc;
+      }
+      acc += q;
+    }
+    if (owner != p.shard_index) {  // uniform over the workgroup
+      if (tid == 0) p.sh_out_picks[row] = dsv41_full_pick{-1, NEG_INF, -1.0f};
+      return;
+    }
+  }
+  // Thread t forms the masses of the contiguous run of chunks [cb, ce) (one chunk per
+  // thread up to 1024 chunks) and their sum `own`; a block scan of the sums gives every
+  // thread S and its run's exclusive prefix `before`.  The inverse-CDF target t = (S U) >> 32
+  // lies in the first chunk whose cumulative Q exceeds it, which the one thread whose run
+  // holds t records; inside that chunk the id boundaries in Q units are
+  // floor(prefix(w) g_c / 2^43) + prefix(history masses), in vocabulary order.
+  uint64_t S = 0;
   if constexpr (DRAW != DRAW_SHARD_RACE && MASSES) {  // the race over slices takes the gathered states
-    for (int c = tid; c < NE; c += NT) {
+    const int crun = (NE + NT - 1) / NT;
+    const int cb = min(tid * crun, NE), ce = min(cb + crun, NE);
+    uint64_t own = 0;
+    for (int c = cb; c < ce; ++c) {
       uint64_t q = scale_mass((uint64_t)cqd[c], mass_ff(em[c], Mref));
       if (p.has_pen) {
         const int s1 = rank_below(h, min((c + 1) * MASS_CHUNK, p.V), p.words, U);
         for (int s = rank_below(h, c * MASS_CHUNK, p.words, U); s < s1; ++s) q += mass_of(penz[s], Mref);
       }
       cq[c] = q;
+      own += q;
     }
+    if (PLACES && tid == 0) m->bi[0] = -1;  // no chunk holds the target (no mass at all)
+    const uint64_t incl = wave_incl_scan_u64(own, lane);
+    if (lane == 63) m->ru[wid] = incl;
     __syncthreads();
+    // lane w reads wave w's total; their scan gives S and the totals of the waves before
+    // this one (one read per lane: a loop over the totals keeps them all in registers)
+    const uint64_t wtot = wave_incl_scan_u64(lane < NW ? m->ru[lane] : 0, lane);
+    S = rl_u64(wtot, NW - 1);
+    uint64_t before = incl - own + (wid > 0 ? rl_u64(wtot, wid - 1) : 0);
+    if constexpr (PLACES) {
+      if constexpr (DRAW == DRAW_CDF) tq = draw_target(u, S);
+      if (before <= tq && tq < before + own) {
+        for (int c = cb; c < ce; ++c) {  // this thread's own chunk masses
+          if (tq < before + cq[c]) {
+            m->bi[0] = c;
+            m->bu[0] = tq - before;
+            break;
+          }
+          before += cq[c];
+        }
+      }
+      __syncthreads();
+    }
   }
-  // S in wave 0: lane l sums the contiguous run of chunks [rb, re), then a wave scan (every
-  // lane returns S, `own` its run and `incl` the run's inclusive prefix)
-  const int run = (NE + 63) / 64;
-  const int rb = min(lane * run, NE), re = min(rb + run, NE);
-  auto mass_scan = [&](uint64_t& own, uint64_t& incl) {
-    uint64_t s = 0;
-    for (int c = rb; c < re; ++c) s += cq[c];
-    own = s;
-    incl = wave_incl_scan_u64(s, lane);
-    return __shfl(incl, 63);
-  };
-  auto row_lp = [&](float ztok, uint64_t S) {
-    return (float)(((double)ztok - (double)M) - log((double)S * 0x1p-43));
+  auto row_lp = [&](float ztok, uint64_t total) {
+    return (float)(((double)ztok - (double)M) - log((double)total * 0x1p-43));
   };
 
   if constexpr (DRAW == DRAW_REPLAY) {
     // the given token's processed log-prob (a separate instantiation, like the race)
-    if (wid == 0) {
-      uint64_t own, incl;
-      const uint64_t S = mass_scan(own, incl);
-      if (lane == 0) {
-        const int64_t tok = p.replay[row];
-        float lp = __builtin_nanf("");
-        if (tok >= 0 && tok < p.V) {
-          const int t = (int)tok;
-          const bool pen = p.has_pen && ((h.bitmap[t >> 5] >> (t & 31)) & 1u);
-          const float ztok = pen ? penz[slot_of(h, t)] : load_one<TIn>(rs, t) / p.T;
-          lp = row_lp(ztok, S);
-        } else {
-          m->status |= ST_BAD_TARGET;
-        }
-        write_result(p, row, m, tok, lp, p.V);
+    if (tid == 0) {
+      const int64_t tok = p.replay[row];
+      float lp = __builtin_nanf("");
+      if (tok >= 0 && tok < p.V) {
+        const int t = (int)tok;
+        const bool pen = p.has_pen && ((h.bitmap[t >> 5] >> (t & 31)) & 1u);
+        const float ztok = pen ? penz[slot_of(h, t)] : load_one<TIn>(rs, t) / p.T;
+        lp = row_lp(ztok, S);
+      } else {
+        m->status |= ST_BAD_TARGET;
       }
+      write_result(p, row, m, tok, lp, p.V);
     }
     return;
   }
@@ -1244,19 +1302,13 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
     // sum differs, which moves every p by the same factor and can reorder only ratios
     // within an ulp of each other.
     float Mr = M;  // the row's maximum (a slice: over all slices)
-    double S;      // the row's sum of exp(z - Mr)
+    double Sr;     // the row's sum of exp(z - Mr)
     if constexpr (DRAW == DRAW_SHARD_RACE) {
-      combine_states(p.sh_states, p.n_shards, p.nrows, row, Mr, S);
+      combine_states(p.sh_states, p.n_shards, p.nrows, row, Mr, Sr);
     } else {
-      if (wid == 0) {
-        uint64_t own, incl;
-        const uint64_t St = mass_scan(own, incl);
-        if (lane == 0) m->bu[1] = St;
-      }
-      __syncthreads();
-      S = (double)m->bu[1] * 0x1p-43;
+      Sr = (double)S * 0x1p-43;
     }
-    const float lsum = Mr + logf((float)S);
+    const float lsum = Mr + logf((float)Sr);
     const float* erow = p.exps + (int64_t)row * p.estride;
     const __amdgpu_buffer_rsrc_t re = row_rsrc(erow, (uint32_t)p.V * 4u);
     float best = -1.0f;
@@ -1338,78 +1390,15 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
         const bool pen = p.has_pen && ((h.bitmap[bi >> 5] >> (bi & 31)) & 1u);
         ztok = pen ? penz[slot_of(h, bi)] : load_one<TIn>(rs, bi) / p.T;
       }
-      write_result(p, row, m, tok, row_lp(ztok, m->bu[1]), p.V);
+      write_result(p, row, m, tok, row_lp(ztok, S), p.V);
     }
     return;
   }
 
-  // The inverse-CDF target t = (S U) >> 32 picks the first chunk whose cumulative Q exceeds
-  // it; inside that chunk the id boundaries in Q units are floor(prefix(w) g_c / 2^43) +
-  // prefix(history masses), in vocabulary order.
-  const float u = PLACES ? row_uniform(p, row, m) : 0.0f;
-  uint64_t tq = 0;  // the draw's target in this workgroup's masses
-  if constexpr (DRAW == DRAW_SHARD_CDF) {
-    // Every slice finds, from the same gathered masses, the slice whose masses hold the
-    // target; only that one places the token, against the target less the masses before it.
-    uint64_t S = 0;
-    for (int s = 0; s < p.n_shards; ++s) S += p.sh_masses[(int64_t)s * p.nrows + row];
-    const uint64_t t = draw_target(u, S);
-    uint64_t acc = 0;
-    int owner = -1;
-    for (int s = 0; s < p.n_shards; ++s) {
-      const uint64_t q = p.sh_masses[(int64_t)s * p.nrows + row];
-      if (owner < 0 && t < acc + q) {
-        owner = s;
-        tq = t - acc;
-      }
-      acc += q;
-    }
-    if (owner != p.shard_index) {  // uniform over the workgroup
-      if (tid == 0) p.sh_out_picks[row] = dsv41_full_pick{-1, NEG_INF, -1.0f};
-      return;
-    }
-  }
   if constexpr (DRAW == DRAW_SHARD_MASS) {
     // this slice's exact mass against the gathered maximum; the draw step gathers them
-    if (wid == 0) {
-      uint64_t s = 0;
-      for (int c = lane; c < NE; c += 64) s += cq[c];
-      s = wave_sum_u64(s);
-      if (lane == 0) p.sh_out_masses[row] = s;
-    }
+    if (tid == 0) p.sh_out_masses[row] = S;
     return;
-  }
-  if (MASSES && wid == 0) {
-    uint64_t own, qincl;
-    const uint64_t S = mass_scan(own, qincl);  // the log-prob's total
-    if constexpr (PLACES) {
-      // the chunk holding the target, from the runs' prefixes
-      if constexpr (DRAW == DRAW_CDF) tq = draw_target(u, S);
-      int cstar = -1;
-      uint64_t need = 0;
-      uint64_t before = qincl - own;
-      if (before <= tq && tq < qincl) {
-        for (int c = rb; c < re; ++c) {
-          if (tq < before + cq[c]) {
-            cstar = c;
-            need = tq - before;
-            break;
-          }
-          before += cq[c];
-        }
-      }
-      const unsigned long long hit = __ballot(cstar >= 0);
-      if (hit) {
-        const int src_lane = __ffsll((long long)hit) - 1;
-        cstar = __shfl(cstar, src_lane);
-        need = __shfl(need, src_lane);
-      }
-      if (lane == 0) {
-        m->bi[0] = cstar;  // -1: no mass at all (a row without a finite maximum)
-        m->bu[0] = need;
-      }
-    }
-    if (lane == 0) m->bu[1] = S;
   }
   // first chunk whose maximum is the row maximum, first history token at it (greedy; a
   // uniform condition, so the block reductions inside are reached by every thread or none)
@@ -1424,7 +1413,6 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
   }
 
   if (wid == 0) {
-    const uint64_t S = m->bu[1];
     int64_t tok = 0;
     float ztok = M;
     // one chunk re-read: z of its elements, history tokens restored from penz
