@@ -40,8 +40,8 @@ BF16_PEAK_TFLOPS = 2500.0
 # counts are in the profiles/ summaries of each kernel and workload.
 MEASURED_TRAFFIC = {
     "sampler_E": 2_629_506_528 + 1_937_544,  # topk_kernel + select_kernel
-    "sampler_B": 83_074_458 + 32_768,  # full_kernel (profiles/sampler_full_B.md)
-    "sampler_E_full": 2_500_916_102 + 4_750_399,  # full_kernel (profiles/sampler_full_E_shape.md)
+    "sampler_B": 82_981_683 + 32_768,  # full_kernel (profiles/sampler_full_B.md)
+    "sampler_E_full": 2_500_868_710 + 2_671_616,  # full_kernel (profiles/sampler_full_E_shape.md)
     "sampler_A": 5_004_270 + 393_216 + 79_872,  # sliced topk_kernel + merge_kernel
     "logprob_D": 46_112_195_686 + 1_048_576,
     "logprob_C": 7_592_285_070 + 1_245_184,  # fused_kernel + merge_kernel
