@@ -674,6 +674,64 @@ def test_small_full_batches_spread_over_the_gpu(rows, V, dtype, greedy):
         assert torch.equal(rep.view(torch.int32), small.logprobs[okr].view(torch.int32))
 
 
+@pytest.mark.parametrize("rows,V,dtype,plens", [(1, 151936, torch.float32, False), (3, 151936, torch.bfloat16, True),
+                                                (8, 129280, torch.float32, True), (100, 5003, torch.float32, False),
+                                                (128, 1000, torch.bfloat16, False)])
+@pytest.mark.parametrize("greedy", [False, True])
+def test_small_full_batches_with_penalties_spread_over_the_gpu(rows, V, dtype, plens, greedy):
+    """Penalized full-vocabulary batches of at most 128 rows take the spread path too: each
+    slice marks its range's history ids from the row's list, and the finishing workgroup
+    builds the history tables and gathers the penalized logits.  Ids, kept sets, statuses
+    and log-probs equal, bit for bit, those of the same rows inside a 200-row batch (one
+    workgroup per row), and the oracle's; replaying each drawn token under the same
+    penalties returns its log-prob bit for bit.  The histories hold repeats, ids at the
+    first and last vocabulary ids and at 256- and 512-id boundaries (span and mass-chunk
+    edges), padding past each row's length, an id past the vocabulary (flagged), a NaN on a
+    history token and one elsewhere (both flagged)."""
+    from dsv41_rocm import replay_log_probs
+    g = torch.Generator().manual_seed(rows * 11 + V)
+    x = (2.0 * torch.randn(200, V, generator=g)).to(dtype)
+    u = torch.rand(200, generator=g)
+    L = 48
+    hist = torch.randint(0, V, (200, L), generator=g)
+    hist[:, :6] = torch.tensor([0, V - 1, min(255, V - 1), min(256, V - 1), min(511, V - 1), min(512, V - 1)])
+    hist[:, 6:12] = hist[:, 12:18]  # repeats
+    hlens = torch.randint(L // 2, L + 1, (200,), generator=g, dtype=torch.int32)
+    hist[torch.arange(L)[None, :] >= hlens[:, None].long()] = -1  # padding past each length
+    pl = torch.randint(0, 8, (200,), generator=g, dtype=torch.int32) if plens else None
+    r_bad_hist = min(1, rows - 1) if rows > 1 else 150
+    hist[r_bad_hist, 0] = V + 5
+    r_nan_hist = min(2, rows - 1) if rows > 2 else 151
+    x[r_nan_hist, int(hist[r_nan_hist, 20])] = float("nan")
+    r_nan = min(3, rows - 1) if rows > 3 else 152
+    x[r_nan, V // 3] = float("nan")
+    knobs = dict(temperature=0.7, repetition_penalty=1.3, presence_penalty=0.4, frequency_penalty=0.3)
+    xd, ud, hd, ld = x.to(DEV), u.to(DEV), hist.to(DEV), hlens.to(DEV)
+    pld = None if pl is None else pl.to(DEV)
+    print(f"case: spread penalized FULL batch rows={rows} V={V} dtype={dtype} plens={plens} greedy={greedy}",
+          flush=True)
+    small = sample(xd[:rows], uniforms=None if greedy else ud[:rows], history=hd[:rows], history_lens=ld[:rows],
+                   history_prompt_lens=None if pld is None else pld[:rows], greedy=greedy, check=False, **knobs)
+    whole = sample(xd, uniforms=None if greedy else ud, history=hd, history_lens=ld, history_prompt_lens=pld,
+                   greedy=greedy, check=False, **knobs)
+    torch.cuda.synchronize()
+    for name in ("ids", "kept", "status"):
+        assert torch.equal(getattr(small, name), getattr(whole, name)[:rows]), name
+    ok = small.status == 0
+    assert torch.equal(small.logprobs[ok].view(torch.int32), whole.logprobs[:rows][ok].view(torch.int32))
+    ora = oracle.sample(x[:rows].float().numpy(), uniforms=None if greedy else u[:rows].numpy(),
+                        history=hist[:rows].numpy(), history_lens=hlens[:rows].numpy(),
+                        history_prompt_lens=None if pl is None else pl[:rows].numpy(), greedy=greedy, **knobs)
+    assert_exact(tuple(t.cpu().numpy() for t in (small.ids, small.logprobs, small.kept, small.status)), ora)
+    if rows > 3:
+        assert int(small.status[r_bad_hist]) != 0 and int(small.status[r_nan]) != 0
+    if bool(ok.any()):
+        okr = ok.nonzero().flatten()
+        rep = replay_log_probs(xd[:rows][okr], small.ids[okr], history=hd[:rows][okr], history_lens=ld[:rows][okr],
+                               history_prompt_lens=None if pld is None else pld[:rows][okr], check=False, **knobs)
+        assert torch.equal(rep.view(torch.int32), small.logprobs[okr].view(torch.int32))
+
+
 @pytest.mark.parametrize("case", ["B_greedy", "small_greedy_fp32", "small_greedy_bf16", "B_cdf", "B_race",
                                   "E_topk", "E_deferred", "A_sliced"])
 def test_sampling_without_logprobs(case):

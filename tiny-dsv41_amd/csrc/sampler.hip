@@ -101,8 +101,9 @@ constexpr int DRAW_ARGMAX = 8;      // first largest logit without its log-prob:
 // Exact masses of the inverse-CDF draws are formed per chunk of MASS_CHUNK consecutive ids
 // of the row (or slice), against the chunk's own maximum.
 constexpr int MASS_CHUNK = 256;
-// FULL batches of at most this many rows without penalties are spread over the GPU
+// FULL batches of at most this many rows are spread over the GPU
 constexpr int PRE_MAX_ROWS = 128;
+constexpr size_t PRE_MAX_LDS = 48 * 1024;  // a spread slice's history bitmap
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -729,12 +730,14 @@ __device__ __forceinline__ void unpack(const Raw<TIn, G>& r, float (&x)[G]) {
 }
 
 // z for G logits at [base, base+G).  History tokens and (TAIL) indices >= V become
-// -inf; the exact values of history tokens come from the batch gather instead.
+// -inf; the exact values of history tokens come from the batch gather instead.  `bitmap`
+// holds the history bits of ids from bit_off on (a multiple of 32).
 template <int G, bool TAIL>
 __device__ __forceinline__ void make_z(const float (&x)[G], int base, const Params& p,
-                                       const uint32_t* bitmap, float (&z)[G], int& bad) {
+                                       const uint32_t* bitmap, float (&z)[G], int& bad, int bit_off = 0) {
   uint32_t pen = 0;
-  if (p.has_pen && (!TAIL || base < p.V)) pen = (bitmap[base >> 5] >> (base & 31)) & ((1u << G) - 1u);
+  if (p.has_pen && (!TAIL || base < p.V))
+    pen = (bitmap[(base - bit_off) >> 5] >> (base & 31)) & ((1u << G) - 1u);
   // a non-finite logit outside the history and inside the row flags the row (history ids are
   // checked where their penalized value is formed; ids past the row read 0)
   auto check = [&](const float (&v)[G]) {
@@ -1014,15 +1017,19 @@ __device__ __forceinline__ double rl_d(double v, int lane) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// A small batch without penalties spread over the GPU: workgroup b takes slice b % n_slices
-// (slice_w wave spans of 64 G ids) of row b / n_slices, one span per wave at a time, and
-// writes the span statistics full_kernel's stream forms (span_stats on the same z), so
-// full_kernel<..., PRE> finishes each row with the values and the order of the one-workgroup
-// kernel: the same ids and log-probs, bit for bit.
+// A small batch spread over the GPU: workgroup b takes slice b % n_slices (slice_w wave
+// spans of 64 G ids) of row b / n_slices, one span per wave at a time, and writes the span
+// statistics full_kernel's stream forms (span_stats on the same z), so full_kernel<...,
+// PRE> finishes each row with the values and the order of the one-workgroup kernel: the
+// same ids and log-probs, bit for bit.  With penalties the slice first marks the history
+// ids of its own range in an LDS bitmap (2 G words per span) from the row's history list,
+// so its history tokens read -inf as in the stream; their penalized values are the
+// finishing kernel's.
 constexpr int PRE_NT = 256;
 template <typename TIn, int G, bool VEC, bool MASSES = true>
 __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
   constexpr int NW = PRE_NT / 64;
+  extern __shared__ __align__(16) unsigned char smem[];
   const int row = blockIdx.x / p.n_slices, sl = blockIdx.x % p.n_slices;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int NC = n_chunks<G>(p.V), NE = n_mass_chunks(p.V);
@@ -1034,6 +1041,21 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
   int c = sl * p.slice_w + wid;
   Raw<TIn, G> A;
   if (c < c1) load_group<TIn, G, VEC, FULL_CPOL>(A, rs, c * 64 * G + lane * G);
+  uint32_t* sbm = reinterpret_cast<uint32_t*>(smem);  // history bits of ids [v0, v0 + 32 words)
+  const int v0 = sl * p.slice_w * 64 * G;
+  if (p.has_pen) {
+    const int words = p.slice_w * 2 * G;
+    for (int i = tid; i < words; i += PRE_NT) sbm[i] = 0;
+    __syncthreads();
+    const int64_t* hr = p.hist + (int64_t)row * p.hstride;
+    const int hl = max(0, min(p.hlens ? p.hlens[row] : p.hlen, (int)p.hstride));
+    const int64_t v1 = min((int64_t)c1 * 64 * G, (int64_t)p.V);
+    for (int i = tid; i < hl; i += PRE_NT) {
+      const int64_t g = hr[i];
+      if (g >= v0 && g < v1) atomicOr(&sbm[(int)(g - v0) >> 5], 1u << ((int)(g - v0) & 31));
+    }
+    __syncthreads();
+  }
   while (c < c1) {  // uniform per wave; the next span's load is in flight meanwhile
     const int cn = c + NW;
     Raw<TIn, G> B;
@@ -1041,7 +1063,7 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
     const int base = c * 64 * G + lane * G;
     float x[G], z[G];
     unpack(A, x);
-    make_z<G, true>(x, base, p, nullptr, z, bad);  // no penalties here; ids past V read -inf
+    make_z<G, true>(x, base, p, sbm, z, bad, v0);  // history ids and ids past V read -inf
     float mc;
     double rs4 = 0.0;
     span_stats<G, MASSES>(z, lane, mc, rs4);
@@ -1116,7 +1138,10 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
   constexpr bool RUN_MAX = PRE || sizeof(TIn) == 2;
   float lmax = NEG_INF;
   if constexpr (PRE) {
-    // the span statistics full_slice_kernel formed (no penalties on this path)
+    // the span statistics full_slice_kernel formed; with penalties, the history tables and
+    // the history tokens' penalized z, which the slices left out
+    HistIds<HR> hi;
+    load_history<NT, HR>(p, row, hi);
     if (tid == 0) m->status = 0;
     const float* pem = p.pre_em + (int64_t)row * NE;
     const uint64_t* pw = p.pre_w + (int64_t)row * NE;
@@ -1127,6 +1152,16 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
     }
     for (int s = tid; s < p.n_slices; s += NT) bad |= p.pre_st[(int64_t)row * p.n_slices + s];
     __syncthreads();  // status cleared before any thread sets a bit
+    if (p.has_pen) {
+      U = build_history<NT, HR>(p, row, hi, h, m);
+      for (int s = tid; s < U; s += NT) {
+        const float z = pen_z(load_one<TIn>(rs, (int)h.tok[s]), count_of(h, s), p);
+        if (!isfinite(z)) bad = 1;
+        penz[s] = z;
+        lmax = fmaxf(lmax, z);
+      }
+    }
+    landed(hi);  // the ids are read under conditions; end their loads on every path
   } else {
   HistIds<HR> hi;
   load_history<NT, HR>(p, row, hi);
@@ -3194,10 +3229,11 @@ struct Plan {
   // LDS, and the workspace offsets of the slices' keys, counts and statuses
   int slices, slice_w, slice_words, slice_ucap;
   size_t slice_lds, merge_lds, ws_counts, ws_status;
-  // small FULL batch without penalties over pre_slices slices of pre_sw wave spans per row
-  // (full_slice_kernel + full_kernel<..., PRE>), with the workspace offsets of its arrays
+  // small FULL batch over pre_slices slices of pre_sw wave spans per row (full_slice_kernel,
+  // pre_lds bytes of history bitmap, + full_kernel<..., PRE>), with the workspace offsets
+  // of its arrays
   int pre_slices, pre_sw;
-  size_t pre_em, pre_w, pre_st;
+  size_t pre_lds, pre_em, pre_w, pre_st;
 };
 
 // shard: the descriptor describes one vocabulary slice (dsv41_sampler_shard_run); the draw
@@ -3336,20 +3372,23 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
       }
     }
   }
-  // A FULL batch of at most PRE_MAX_ROWS rows without penalties leaves most CUs idle with one
-  // workgroup per row: about 512 workgroups then each take a run of a row's wave spans
-  // (full_slice_kernel), and one workgroup per row finishes it from their statistics.
+  // A FULL batch of at most PRE_MAX_ROWS rows leaves most CUs idle with one workgroup per
+  // row: about 512 workgroups then each take a run of a row's wave spans (full_slice_kernel,
+  // with its range's history bitmap in LDS), and one workgroup per row finishes it from
+  // their statistics.
   pl->pre_slices = 0;
-  if (!shard && pl->mode == MODE_FULL && !pl->has_pen && !d->replay_ids && !d->exponentials &&
-      d->rows <= PRE_MAX_ROWS) {
+  pl->pre_lds = 0;
+  if (!shard && pl->mode == MODE_FULL && !d->replay_ids && !d->exponentials && d->rows <= PRE_MAX_ROWS) {
     const int G = pl->esize == 4 ? 4 : 8;  // the spread small batches take 4 fp32 logits per lane
     const int NC = (V + 64 * G - 1) / (64 * G), NE = n_mass_chunks(V);
     const int want = std::max(2, 512 / d->rows);
     const int sw = std::max(PRE_NT / 64, (NC + want - 1) / want);  // at least one span per wave
     const int S = (NC + sw - 1) / sw;
-    if (S >= 2) {
+    const size_t slds = pl->has_pen ? (size_t)sw * 2 * G * sizeof(uint32_t) : 0;
+    if (S >= 2 && slds <= PRE_MAX_LDS) {
       pl->pre_slices = S;
       pl->pre_sw = sw;
+      pl->pre_lds = slds;
       size_t off = align16(pl->workspace);
       pl->pre_em = off;
       off = align16(off + (size_t)d->rows * NE * sizeof(float));
@@ -3516,22 +3555,24 @@ static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params
 static int run_presliced(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, hipStream_t s) {
   const dim3 grid(d->rows * pl.pre_slices), block(PRE_NT);
   const bool bf = pl.esize == 2, ex = !p.greedy, lp = p.out_lp != nullptr;
-  // no dynamic LDS (a little static LDS for the block vote): no attribute to raise
+  // the history bitmap (at most PRE_MAX_LDS bytes) stays under the default dynamic LDS
+  // limit: no attribute to raise
+  const size_t sl = pl.pre_lds;
   if (bf) {
     if (lp) {
-      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false>), grid, block, 0, s, p);
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true>), grid, block, sl, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false>), grid, block, sl, s, p);
     } else {
-      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, false>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, false>), grid, block, 0, s, p);
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, true, false>), grid, block, sl, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<uint16_t, 8, false, false>), grid, block, sl, s, p);
     }
   } else {
     if (lp) {
-      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false>), grid, block, 0, s, p);
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true>), grid, block, sl, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false>), grid, block, sl, s, p);
     } else {
-      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true, false>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false, false>), grid, block, 0, s, p);
+      if (pl.vec) hipLaunchKernelGGL((full_slice_kernel<float, 4, true, false>), grid, block, sl, s, p);
+      else hipLaunchKernelGGL((full_slice_kernel<float, 4, false, false>), grid, block, sl, s, p);
     }
   }
   DSV41_HIP_CHECK(hipGetLastError());
