@@ -117,6 +117,15 @@ template <int CTRL, int ROWS = 0xF>
 __device__ __forceinline__ uint64_t dpp_scan_u64(uint64_t v) {
   return ((uint64_t)dpp_scan_u32<CTRL, ROWS>((uint32_t)(v >> 32)) << 32) | dpp_scan_u32<CTRL, ROWS>((uint32_t)v);
 }
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += dpp_scan_u32<0x111>(v);        // row_shr:1
+  v += dpp_scan_u32<0x112>(v);        // row_shr:2
+  v += dpp_scan_u32<0x114>(v);        // row_shr:4
+  v += dpp_scan_u32<0x118>(v);        // row_shr:8
+  v += dpp_scan_u32<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_scan_u32<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+  return v;
+}
 __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
   (void)lane;
   v += dpp_scan_u64<0x111>(v);        // row_shr:1

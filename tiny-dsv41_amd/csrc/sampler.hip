@@ -635,18 +635,18 @@ __device__ __forceinline__ int build_history(const Params& p, int row, const His
   const int b = tid * per, e = min(b + per, W);
   int s = 0;
   for (int i = b; i < e; ++i) s += __popc(h.bitmap[i]);
-  const int incl = wave_incl_scan_i(s, lane);
+  const int incl = (int)wave_incl_scan_u32((uint32_t)s);
   if (lane == 63) m->ri[wid] = incl;
   __syncthreads();
-  int off = 0;
-  for (int i = 0; i < wid; ++i) off += m->ri[i];
+  // lane w reads wave w's count; their scan gives the slots before this wave and U
+  const int wtot = (int)wave_incl_scan_u32(lane < NW ? (uint32_t)m->ri[lane] : 0u);
+  const int off = wid > 0 ? __builtin_amdgcn_readlane(wtot, wid - 1) : 0;
+  const int U = __builtin_amdgcn_readlane(wtot, NW - 1);
   int run = off + incl - s;
   for (int i = b; i < e; ++i) {
     h.wrank[i] = (uint16_t)run;
     run += __popc(h.bitmap[i]);
   }
-  int U = 0;
-  for (int i = 0; i < NW; ++i) U += m->ri[i];
   __syncthreads();
   auto count_id = [&](int64_t g, int idx) {
     const int64_t id = g - id_off;
@@ -1172,8 +1172,9 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
         if (tid == 0) m->status = 0;
         if constexpr (MASSES)
           for (int e = tid; e < NE; e += NT) cq[e] = 0;
-        __syncthreads();
+        // the history build's first barrier also publishes the cleared status and masses
         if (p.has_pen) U = build_history<NT, HR, SLICE>(p, row, hi, h, m);
+        else __syncthreads();
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
@@ -1589,6 +1590,8 @@ __device__ __forceinline__ uint64_t kth_largest(const uint64_t* keys, int n, int
         c[q] = cnt[255 - (lane * 4 + q)];
         sum += c[q];
       }
+      // (shuffles, not the DPP scan: with DPP here topk_kernel's scalar spills move from
+      // vector-register lanes to scratch memory)
       const uint32_t incl = (uint32_t)wave_incl_scan_i((int)sum, lane);
       const uint32_t before = incl - sum;
       if (before < target && target <= incl) {
