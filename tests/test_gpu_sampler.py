@@ -639,13 +639,33 @@ def test_largest_vocabulary(V, dtype, knobs):
     assert (ora[3] == 0).all()
 
 
+@pytest.mark.parametrize("dtype,knobs", [(torch.float32, dict()),
+                                          (torch.bfloat16, dict(frequency_penalty=0.2, presence_penalty=0.3))])
+def test_full_draw_with_more_chunks_than_threads(dtype, knobs):
+    """130 rows of 300,007 ids (one workgroup per row: more than 128 rows) hold 1172 mass
+    chunks, more than the workgroup's 1024 threads, so each thread combines a run of two
+    chunks before the workgroup-wide scan; ids, kept sets, statuses and log-probs match the
+    oracle.  Flat rows, a maximum at the last id and one at the first id of the second run."""
+    rows, V = 130, 300_007
+    g = torch.Generator().manual_seed(1172)
+    x = 2.0 * torch.randn(rows, V, generator=g)
+    x[1] = 0.0
+    x[2, V - 1] = 25.0
+    x[3, 2 * 256] = 25.0
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, 64), generator=g)
+    gpu, ora = run_both(x.to(dtype), u, hist if knobs else None, temperature=0.9, **knobs)
+    assert_exact(gpu, ora)
+    assert (ora[3] == 0).all()
+
+
 @pytest.mark.parametrize("rows,V,dtype", [(1, 151936, torch.float32), (3, 151936, torch.bfloat16),
                                           (8, 129280, torch.float32), (100, 5003, torch.float32),
                                           (128, 1000, torch.bfloat16)])
 @pytest.mark.parametrize("greedy", [False, True])
 def test_small_full_batches_spread_over_the_gpu(rows, V, dtype, greedy):
-    """Full-vocabulary batches of at most 128 rows without penalties are spread over the GPU
-    (slices of wave spans, then one finishing workgroup per row).  Their ids and log-probs
+    """Full-vocabulary batches of at most 128 rows are spread over the GPU (slices of wave
+    spans, then one finishing workgroup per row).  Their ids and log-probs
     equal, bit for bit, those of the same rows drawn inside a 200-row batch (one workgroup
     per row, the stream of the same kernel), and the oracle's; the replay of every drawn
     token returns the drawn log-prob bit for bit."""
