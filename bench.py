@@ -39,10 +39,10 @@ BF16_PEAK_TFLOPS = 2500.0
 # the same counters on a plain 1 GiB copy (FETCH x 2.0, WRITE x 1.0); the commands and raw
 # counts are in the profiles/ summaries of each kernel and workload.
 MEASURED_TRAFFIC = {
-    "sampler_E": 2_629_506_528 + 1_937_544,  # topk_kernel + select_kernel
+    "sampler_E": 2_627_486_720 + 1_852_211,  # topk_kernel + select_kernel (profiles/sampler_topk_E.md)
     "sampler_B": 82_981_683 + 32_768,  # full_kernel (profiles/sampler_full_B.md)
     "sampler_E_full": 2_500_868_710 + 2_671_616,  # full_kernel (profiles/sampler_full_E_shape.md)
-    "sampler_A": 5_004_270 + 393_216 + 79_872,  # sliced topk_kernel + merge_kernel
+    "sampler_A": 4_951_450 + 318_464 + 79_872,  # sliced topk_kernel + merge_kernel (profiles/sampler_topk_A.md)
     "logprob_D": 46_112_195_686 + 1_048_576,
     "logprob_C": 7_592_285_070 + 1_245_184,  # fused_kernel + merge_kernel
     "logprob_grad_D": 45_297_095_573 + 4_384_320_091,
