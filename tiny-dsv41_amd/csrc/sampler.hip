@@ -2248,25 +2248,34 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
           }
           wm = uni(fmaxf(wm, wave_max_dpp(pz)));
         }
-        const uint64_t kg = ckey(zg, tg);
-        bal[NE - 1] = __ballot(zg > NEG_INF && kg > tk && zg >= bnd);
-        wn += (uint32_t)__popcll(bal[NE - 1]);
+        // the batch's gathered history slot (none when the batch gathered none: zg = -inf)
+        uint64_t kg = 0;
+        bal[NE - 1] = 0;
+        if (n > 0) {
+          kg = ckey(zg, tg);
+          bal[NE - 1] = __ballot(zg > NEG_INF && kg > tk && zg >= bnd);
+          wn += (uint32_t)__popcll(bal[NE - 1]);
+        }
         int total;
         int pos = exchange(wn, total);
         if (pos >= 0) {
-#pragma unroll
-          for (int e = 0; e < NE; ++e) {
-            if (bal[e]) {
-              if ((bal[e] >> lane) & 1ull) {
-                const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[e] >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal[e], 0u));
-                const uint64_t key =
-                    e == NE - 1 ? kg : ckey(x[e / G][e % G], (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
-                cand[pos + below] = key;
-              }
-              pos += (int)__popcll(bal[e]);
+          auto insert = [&](int e, uint64_t b) {
+            if ((b >> lane) & 1ull) {
+              const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+              const uint64_t key =
+                  e == NE - 1 ? kg : ckey(x[e / G][e % G], (uint32_t)((t0 + e / G) * TILE + tid * G + e % G));
+              cand[pos + below] = key;
             }
+            pos += (int)__popcll(b);
+          };
+          // the stream elements' ballots are all zero when nothing passed: the common
+          // batch then reads none of them back
+          if (any) {
+#pragma unroll
+            for (int e = 0; e < NE - 1; ++e)
+              if (bal[e]) insert(e, bal[e]);
           }
+          if (bal[NE - 1]) insert(NE - 1, bal[NE - 1]);
           count += total;
         } else {
           // the batch does not fit: one round per tile, then the history round; each
