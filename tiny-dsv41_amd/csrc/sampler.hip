@@ -2015,7 +2015,10 @@ __device__ __forceinline__ void block_final(const Params& p, int row, Misc* m, u
 // SLICED (with EMIT): a batch too small to fill the GPU, spread over it.  Each workgroup
 // emits its slice's exact local top_k, as a vocabulary shard does, into
 // [n_slices, nrows, emit_cap]; merge_kernel then finishes every row exactly.
-template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT, bool SLICED = false>
+// GATHER = false: a batch that gathers no history slots (no penalties, or lowering ones,
+// which the stream applies itself), whose batch loop then holds no gathered-slot code:
+// fewer live registers on every batch.
+template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT, bool SLICED = false, bool GATHER = true>
 __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
   static_assert(!SLICED || EMIT, "a sliced launch emits candidate lists");
   const int row = SLICED ? (int)blockIdx.x / p.n_slices : (int)blockIdx.x;
@@ -2121,7 +2124,8 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         landed(hi);  // the ids are read under conditions; end their loads on every path
         return U;
       },
-      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n_gathered, float gx) {
+        const int n = GATHER ? n_gathered : 0;
         // Tiles past the row are read and masked, not skipped, so that every load is
         // consumed (as in full_kernel).
         float x[PF][G];
@@ -3564,6 +3568,14 @@ static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params
 }
 
 // A small FULL batch: the slices' statistics, then one finishing workgroup per row.
+// One workgroup per row of a top-k batch: the instantiation without gathered-slot code when
+// the batch gathers no history slots (no penalties, or lowering penalties).
+template <typename TIn, bool VEC, int NT>
+static int launch_topk_rows(size_t lds, int rows, const Params& q, hipStream_t s) {
+  if (q.has_pen && !q.pen_lowers) return launch(topk_kernel<TIn, VEC, false, NT>, NT, lds, rows, q, s);
+  return launch(topk_kernel<TIn, VEC, false, NT, false, false>, NT, lds, rows, q, s);
+}
+
 static int run_presliced(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, hipStream_t s) {
   const dim3 grid(d->rows * pl.pre_slices), block(PRE_NT);
   const bool bf = pl.esize == 2, ex = !p.greedy, lp = p.out_lp != nullptr;
@@ -3649,16 +3661,16 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
           q.ucap = 0;
           q.no_ranks = 1;
         }
-        if (bf) rc = pl.vec ? launch(topk_kernel<uint16_t, true, false, 256>, 256, pl.lds, d->rows, q, s)
-                            : launch(topk_kernel<uint16_t, false, false, 256>, 256, pl.lds, d->rows, q, s);
-        else rc = pl.vec ? launch(topk_kernel<float, true, false, 256>, 256, pl.lds, d->rows, q, s)
-                         : launch(topk_kernel<float, false, false, 256>, 256, pl.lds, d->rows, q, s);
+        if (bf) rc = pl.vec ? launch_topk_rows<uint16_t, true, 256>(pl.lds, d->rows, q, s)
+                            : launch_topk_rows<uint16_t, false, 256>(pl.lds, d->rows, q, s);
+        else rc = pl.vec ? launch_topk_rows<float, true, 256>(pl.lds, d->rows, q, s)
+                         : launch_topk_rows<float, false, 256>(pl.lds, d->rows, q, s);
       } else if (bf) {
-        rc = pl.vec ? launch(topk_kernel<uint16_t, true>, TOPK_NT, pl.lds, d->rows, p, s)
-                    : launch(topk_kernel<uint16_t, false>, TOPK_NT, pl.lds, d->rows, p, s);
+        rc = pl.vec ? launch_topk_rows<uint16_t, true, TOPK_NT>(pl.lds, d->rows, p, s)
+                    : launch_topk_rows<uint16_t, false, TOPK_NT>(pl.lds, d->rows, p, s);
       } else {
-        rc = pl.vec ? launch(topk_kernel<float, true>, TOPK_NT, pl.lds, d->rows, p, s)
-                    : launch(topk_kernel<float, false>, TOPK_NT, pl.lds, d->rows, p, s);
+        rc = pl.vec ? launch_topk_rows<float, true, TOPK_NT>(pl.lds, d->rows, p, s)
+                    : launch_topk_rows<float, false, TOPK_NT>(pl.lds, d->rows, p, s);
       }
       if (rc != DSV41_OK) return rc;
       if (pl.defer) {
