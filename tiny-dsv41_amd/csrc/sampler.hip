@@ -989,9 +989,8 @@ __device__ __forceinline__ uint64_t scale_mass(uint64_t w, float g) {
 // floor(2^43 exp32(z - mc)), integers of at most 2^43, so the fp64 sums are exact in any
 // order (a chunk's total is below 2^51).
 template <int G, bool MASSES = true>
-__device__ __forceinline__ void span_stats(const float (&z)[G], int lane, float& mc, double& rs4) {
+__device__ __forceinline__ void span_stats(const float (&z)[G], float& mc, double& rs4) {
   static_assert(G == 4 || G == 8, "a mass chunk is the span (G 4) or its half (G 8)");
-  (void)lane;
   float mx = z[0];
 #pragma unroll
   for (int j = 1; j < G; ++j) mx = fmaxf(mx, z[j]);
@@ -1041,7 +1040,7 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
   int c = sl * p.slice_w + wid;
   Raw<TIn, G> A;
   if (c < c1) load_group<TIn, G, VEC, FULL_CPOL>(A, rs, c * 64 * G + lane * G);
-  uint32_t* sbm = reinterpret_cast<uint32_t*>(smem);  // history bits of ids [v0, v0 + 32 words)
+  uint32_t* sbm = reinterpret_cast<uint32_t*>(smem);  // history bits of the slice's ids, from v0 on
   const int v0 = sl * p.slice_w * 64 * G;
   if (p.has_pen) {
     const int words = p.slice_w * 2 * G;
@@ -1066,7 +1065,7 @@ __global__ __launch_bounds__(PRE_NT) void full_slice_kernel(Params p) {
     make_z<G, true>(x, base, p, sbm, z, bad, v0);  // history ids and ids past V read -inf
     float mc;
     double rs4 = 0.0;
-    span_stats<G, MASSES>(z, lane, mc, rs4);
+    span_stats<G, MASSES>(z, mc, rs4);
     const int e = c * (64 * G / MASS_CHUNK) + (G == 4 ? 0 : (lane >> 5));
     if ((G == 4 ? lane : (lane & 31)) == 0 && e < NE) oem[e] = mc;
     if constexpr (MASSES) {
@@ -1190,7 +1189,7 @@ __global__ __launch_bounds__(FULL_NT, sizeof(TIn) == 4 ? 8 : 1) void full_kernel
             else make_z<G, true>(x, base, p, h.bitmap, z, bad);
             float mc;
             double rs4 = 0.0;
-            span_stats<G, MASSES>(z, lane, mc, rs4);
+            span_stats<G, MASSES>(z, mc, rs4);
             if constexpr (RUN_MAX) lmax = fmaxf(lmax, mc);
             // the lane's 256-id chunk: the span, or its half for G = 8
             const int e = (t * TILE + wid * 64 * G) / MASS_CHUNK + (G == 4 ? 0 : (lane >> 5));
