@@ -458,11 +458,56 @@ def test_top_p_alone_three_pass_kernel(dtype, knobs):
         assert (gpu[2][3::8][gpu[3][3::8] == 0] > 4096).all()  # the constant rows went through the fallback
 
 
+@pytest.mark.parametrize("rows,V,dtype,hist_len", [
+    (600, 20011, torch.float32, 0),
+    (520, 50021, torch.bfloat16, 64),
+])
+def test_top_p_alone_two_workgroups_per_cu(rows, V, dtype, hist_len):
+    """Batches of at least 512 rows whose tables fit half a CU's LDS run topp_kernel with
+    512 threads, two workgroups per CU.  Peaked, flat, tied and constant rows take the
+    list, the third read and the radix fallback there as with 1024 threads."""
+    g = torch.Generator().manual_seed(rows)
+    logits = 3.0 * torch.randn(rows, V, generator=g)
+    logits[1::4] = 0.01 * torch.randn(len(range(1, rows, 4)), V, generator=g)             # flat
+    logits[2::4] = torch.randint(-4, 5, (len(range(2, rows, 4)), V), generator=g).float()  # ties
+    logits[3::8] = 0.25                                                                     # constant
+    u = torch.rand(rows, generator=g)
+    hist = torch.randint(0, V, (rows, hist_len), generator=g) if hist_len else None
+    pen = dict(repetition_penalty=1.2, frequency_penalty=0.05) if hist_len else {}
+    gpu, ora = run_both(logits.to(dtype), u, hist, temperature=0.8, top_p=0.9, **pen)
+    assert_exact(gpu, ora)
+    assert (gpu[2][3::8][gpu[3][3::8] == 0] > 4096).all()
+
+
 def test_top_p_alone_config_e_vocabulary():
     inp = workloads.sampler_inputs("E", rows=64)
     gpu, ora = run_both(inp["logits"], inp["uniforms"], inp["history"], temperature=0.6,
                         repetition_penalty=1.05, top_p=0.9)
     assert_exact(gpu, ora)
+
+
+def test_top_p_alone_history_tokens_weigh_exp32_masses():
+    """Penalized history tokens weigh floor(2^43 exp32(d)) in the top-p total, like every
+    other token.  The row: the maximum (z = 0) and eight history tokens that the repetition
+    penalty 2 takes exactly to d = -0.3433722..., where floor(2^43 exp(d)) in fp64 exceeds
+    the exp32 mass by 395,154 units; every other token weighs 0.  top_p is the float at
+    which the exact total keeps eight tokens while a total with fp64 masses would keep
+    nine: the threshold lies in the 8 x 395,154 units between the two totals."""
+    d = np.float32(-0.3433722257614136)
+    m = oracle.mass(d, np.float32(0.0))
+    m64 = int(oracle.exp_det(float(d)) * 2.0 ** 43)
+    assert m64 - m == 395154
+    S, S64, C8 = 2 ** 43 + 8 * m, 2 ** 43 + 8 * m64, 2 ** 43 + 7 * m
+    p = float(np.float32(C8 / S))
+    assert oracle.top_p_threshold(p, S) <= C8 < oracle.top_p_threshold(p, S64)
+    V = 4099
+    logits = torch.full((2, V), -60.0)
+    logits[:, 0] = 0.0
+    logits[:, 1:9] = float(d / np.float32(2.0))
+    history = torch.arange(1, 9).repeat(2, 1)
+    gpu, ora = run_both(logits, torch.tensor([0.5, 0.97]), history, repetition_penalty=2.0, top_p=p)
+    assert_exact(gpu, ora)
+    assert (gpu[2] == 8).all() and (gpu[3] == 0).all()
 
 
 @pytest.mark.parametrize("knobs", [

@@ -2555,10 +2555,11 @@ __global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
 // total over the whole row is needed before any token can be placed.  The row is read
 // two or three times instead of being written to a workspace:
 //   1. z of every token (penalties exact), the row maximum and its first index;
-//   2. every token's exact mass (mass_of, zero below d = z - zmax = -30) into the row
-//      total and into a bin of the float bits of (zmax - z), and the tokens with d at
-//      or above a bound that rises as it fills into an LDS list.  fl(zmax - z) is
-//      monotone in z, so the bins split the descending order into consecutive runs.
+//   2. every token's exact mass (mass_of) into the row total; at or above the depth where
+//      the boundary can lie (topp_depth), into a bin of the float bits of (zmax - z); and
+//      the tokens with d = z - zmax at or above a bound that rises as it fills into an
+//      LDS list.  fl(zmax - z) is monotone in z, so the bins split the descending order
+//      into consecutive runs.
 // The cumulative bin masses then name the bin b* holding the boundary.  Tokens of bins
 // before b* are kept (their masses go to the chunk table, one u64 per 64*G-element chunk
 // as in FULL, and to the exp sum); the tokens of b* are sorted and kept up to the first
@@ -2575,14 +2576,28 @@ __device__ __forceinline__ float topp_list_bound(int c, int cap) {
        : e < 5 ? -3.0f : e < 6 ? -2.0f : -1.0f;
 }
 
+// The depth below which no token can hold the top-p boundary.  A token with
+// d = fl(z - zmax) < D weighs floor(2^43 exp32(d)) < 2^43 e^D (1 + 2^-22), so all V of them
+// weigh less than 2^43 ((1 - p) - 2^-40) <= (1 - p) S - 8 once
+// V e^D (1 + 2^-22) < (1 - p) - 2^-40 (S >= 2^43, the maximum's own mass).  The tokens at
+// or above D then weigh more than p S + 8 > ceil(p S): the boundary and every bin before
+// it lie at or above D, so the bins need no token below it.  Tokens below -31 weigh 0.
+__device__ __forceinline__ float topp_depth(float top_p, int V) {
+  const double a = (1.0 - (double)top_p) - 0x1p-40;
+  if (!(a > 0.0)) return -31.0f;
+  return fmaxf((float)(log(a / ((double)V * 1.0001)) - 0.01), -31.0f);
+}
+
 __device__ __forceinline__ int topp_bin(float z, float zmax) {
   const int b = (int)(__float_as_uint(zmax - z) >> 16) - TOPP_BIN_BASE;
   return min(max(b, 0), TOPP_BINS - 1);
 }
 
-template <typename TIn, int G, bool VEC>
-__global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
-  constexpr int NT = TOPP_NT, HR = 4, TILE = NT * G, CH = 64 * G;
+// NT: TOPP_NT, or 512 where two workgroups fit a CU's LDS (one row's read of the maximum
+// then overlaps the other's mass pass)
+template <typename TIn, int G, bool VEC, int NT = TOPP_NT>
+__global__ __launch_bounds__(NT, 4) void topp_kernel(Params p) {
+  constexpr int HR = 4, TILE = NT * G, CH = 64 * G;
   extern __shared__ __align__(16) unsigned char smem[];
   const Layout L = make_layout<MODE_TOPP, G>(p.V, p.words, p.ucap, p.cap);
   Misc* m = reinterpret_cast<Misc*>(smem + L.misc);
@@ -2658,11 +2673,14 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
   }
   const double dmax = (double)zmax;
 
-  // ---- pass 2: exact masses into the row total and the bins; tokens near the maximum
-  // into the list.  A thread lists a token when d >= its bound db, which only rises with
-  // the list's length, so the list holds every token with d >= (the largest final db).
+  // ---- pass 2: exact masses into the row total; tokens at or above the boundary depth
+  // dstar into the bins, and those near the maximum into the list.  d = fl(z - zmax) is
+  // -fl(zmax - z), the bins' own difference.  A thread lists a token when d >= its bound db,
+  // which only rises with the list's length, so the list holds every token with
+  // d >= (the largest final db).  A tile's G masses (each at most 2^43) sum exactly in fp64.
   uint64_t tot = 0;
-  float db = -16.0f;
+  const float dstar = topp_depth(p.top_p, V);
+  float db = fmaxf(-16.0f, dstar);
   int lost = 0;
   auto offer = [&](float z, int idx) {
     const int pos = atomicAdd(&m->count, 1);
@@ -2681,16 +2699,18 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
             float x[G], z[G];
             unpack(R[k], x);
             make_z<G, true>(x, base, p, h.bitmap, z, bad);
+            double ts = 0.0;
 #pragma unroll
             for (int j = 0; j < G; ++j) {
-              const double d = (double)z[j] - dmax;
-              if (d >= -30.0) {
-                const uint64_t ms = mass_of(z[j], zmax);
-                tot += ms;
-                if (ms) atomicAdd((unsigned long long*)&bins[topp_bin(z[j], zmax)], (unsigned long long)ms);
-                if (d >= (double)db) offer(z[j], base + j);
+              const float ms = mass_ff(z[j], zmax);
+              ts += (double)ms;
+              const float d = z[j] - zmax;
+              if (d >= dstar && ms != 0.0f) {
+                atomicAdd((unsigned long long*)&bins[topp_bin(z[j], zmax)], (unsigned long long)ms);
+                if (d >= db) offer(z[j], base + j);
               }
             }
+            tot += (uint64_t)ts;
             db = fmaxf(db, topp_list_bound(__atomic_load_n(&m->count, __ATOMIC_RELAXED), p.cap));
           }
         }
@@ -2699,12 +2719,12 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
           const int tok = (int)h.tok[s];
           const float x = i == tid ? gx : load_one<TIn>(rs, tok);
           const float z = pen_z(x, count_of(h, s), p);
-          const double d = (double)z - dmax;
-          if (d >= -30.0) {
-            const uint64_t ms = (uint64_t)(exp_det(d) * 8796093022208.0);
-            tot += ms;
-            if (ms) atomicAdd((unsigned long long*)&bins[topp_bin(z, zmax)], (unsigned long long)ms);
-            if (d >= (double)db) offer(z, tok);
+          const uint64_t ms = mass_of(z, zmax);
+          tot += ms;
+          const float d = z - zmax;
+          if (d >= dstar && ms != 0) {
+            atomicAdd((unsigned long long*)&bins[topp_bin(z, zmax)], (unsigned long long)ms);
+            if (d >= db) offer(z, tok);
           }
         }
       });
@@ -2743,7 +2763,8 @@ __global__ __launch_bounds__(TOPP_NT) void topp_kernel(Params p) {
   __syncthreads();
 
   // The list covers bins <= b* when every token there has d >= dbf: such a token has
-  // fl(zmax - z) below the bin's upper edge ub, so d > -ub * (1 + 2^-23).
+  // fl(zmax - z) below the bin's upper edge ub, so d = -fl(zmax - z) > -ub (the test
+  // keeps a margin of 2^-22).
   bool from_list = !lost && bstar >= 0 && bstar < TOPP_BINS - 1;
   if (from_list) {
     const float ub = __uint_as_float((uint32_t)(bstar + TOPP_BIN_BASE + 1) << 16);
@@ -3239,6 +3260,7 @@ struct Plan {
   size_t lds;
   size_t workspace;
   int topk_nt;        // TOPK threads per workgroup: TOPK_NT, or 256 (see plan)
+  int topp_nt;        // TOPP threads per workgroup: TOPP_NT, or 512 (see plan)
   bool bitmap_only;   // TOPK penalties need only the membership bitmap
   // sliced small TOPK batch (slices > 1): slice width, its table sizes and LDS, the merge's
   // LDS, and the workspace offsets of the slices' keys, counts and statuses
@@ -3336,6 +3358,9 @@ int plan(const dsv41_sampler_desc* d, Plan* pl, bool shard = false) {
   if (pl->lds > LDS_LIMIT)
     return fail(DSV41_E_UNSUPPORTED, "history length and vocabulary exceed the on-chip penalty tables");
   pl->defer = !shard && pl->mode == MODE_TOPK && d->rows > DEFER_MIN_ROWS;
+  // Batches of at least two rows per CU whose TOPP tables fit two workgroups per CU run
+  // with 512 threads: a row's first read (memory) then overlaps another's mass pass (ALU).
+  pl->topp_nt = pl->mode == MODE_TOPP && d->rows >= 512 && 2 * pl->lds <= LDS_LIMIT ? 512 : TOPP_NT;
   // Deferred TOPK batches whose tables fit four 256-thread workgroups per CU (a quarter of
   // LDS) run with 256 threads: 128 VGPRs then hold four rows per CU instead of two, so a
   // row building its history tables leaves three others streaming.  Lowering penalties
@@ -3681,10 +3706,18 @@ static int run_planned(const dsv41_sampler_desc* d, const Plan& pl, void* worksp
       return run_flagged(d, pl, p, s);
     }
     case MODE_TOPP:
-      if (bf) rc = pl.vec ? launch(topp_kernel<uint16_t, 4, true>, TOPP_NT, pl.lds, d->rows, p, s)
-                          : launch(topp_kernel<uint16_t, 4, false>, TOPP_NT, pl.lds, d->rows, p, s);
-      else rc = pl.vec ? launch(topp_kernel<float, 4, true>, TOPP_NT, pl.lds, d->rows, p, s)
-                       : launch(topp_kernel<float, 4, false>, TOPP_NT, pl.lds, d->rows, p, s);
+      if (pl.topp_nt == 512) {
+        if (bf) rc = pl.vec ? launch(topp_kernel<uint16_t, 4, true, 512>, 512, pl.lds, d->rows, p, s)
+                            : launch(topp_kernel<uint16_t, 4, false, 512>, 512, pl.lds, d->rows, p, s);
+        else rc = pl.vec ? launch(topp_kernel<float, 4, true, 512>, 512, pl.lds, d->rows, p, s)
+                         : launch(topp_kernel<float, 4, false, 512>, 512, pl.lds, d->rows, p, s);
+      } else if (bf) {
+        rc = pl.vec ? launch(topp_kernel<uint16_t, 4, true>, TOPP_NT, pl.lds, d->rows, p, s)
+                    : launch(topp_kernel<uint16_t, 4, false>, TOPP_NT, pl.lds, d->rows, p, s);
+      } else {
+        rc = pl.vec ? launch(topp_kernel<float, 4, true>, TOPP_NT, pl.lds, d->rows, p, s)
+                    : launch(topp_kernel<float, 4, false>, TOPP_NT, pl.lds, d->rows, p, s);
+      }
       if (rc != DSV41_OK) return rc;
       return run_flagged(d, pl, p, s);
     default:
