@@ -233,12 +233,18 @@ def test_top_k_without_min_p_compacts_before_the_selection(rows, dtype, knobs):
     (300, 20011, torch.float32, dict(top_k=50, repetition_penalty=1.3)),                  # deferred, 256 threads
     (300, 20011, torch.bfloat16, dict(top_k=64, top_p=0.9, repetition_penalty=0.8)),      # raising penalty: gather
     (300, 20011, torch.float32, dict(top_k=1, presence_penalty=0.5, frequency_penalty=0.3)),
+    (300, 20011, torch.float32, dict(top_k=256, repetition_penalty=1.3)),                 # four offers a lane, all used
+    (300, 20011, torch.bfloat16, dict(top_k=257, top_p=0.9)),                             # above the seeded range
+    (300, 600, torch.float32, dict(top_k=200)),                                           # waves with fewer offers than top_k
     (3, 151936, torch.float32, dict(top_k=7, repetition_penalty=1.1)),                    # sliced
     (5, 151936, torch.bfloat16, dict(top_k=50, top_p=0.95)),                              # sliced, bf16 ties
 ])
 def test_top_k_first_batch_threshold(rows, V, dtype, knobs):
-    """Top-k <= 64 without min-p: each wave takes its first threshold from the largest logit
-    of every lane before filtering its first batch.  Rows where that bound meets ties:
+    """Top-k without min-p: a first threshold before filtering the first batch.  Sliced rows
+    (top_k <= 64): each wave takes the top_k-th largest of its lanes' largest logits.
+    Deferred 256-thread batches (top_k <= 256): each wave the top_k-th largest of four
+    offers a lane, and the workgroup the largest of the waves' bounds.  Rows where that
+    bound meets ties:
     integer-valued logits (hundreds of elements share each value), a row whose only
     large logits are history tokens (penalized, so they must not set the bound), rows
     with +inf and NaN in the first batch, and rows of a constant logit."""

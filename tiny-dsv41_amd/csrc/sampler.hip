@@ -2017,7 +2017,10 @@ __device__ __forceinline__ void block_final(const Params& p, int row, Misc* m, u
 // GATHER = false: a batch that gathers no history slots (no penalties, or lowering ones,
 // which the stream applies itself), whose batch loop then holds no gathered-slot code:
 // fewer live registers on every batch.
-template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT, bool SLICED = false, bool GATHER = true>
+// SEED (256-thread row launches of top_k <= 256 without min-p): the first batch's threshold
+// is the largest of the waves' top_k-th largest offers, four per lane, over one barrier.
+template <typename TIn, bool VEC, bool EMIT = false, int NTK = TOPK_NT, bool SLICED = false, bool GATHER = true,
+          bool SEED = false>
 __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
   static_assert(!SLICED || EMIT, "a sliced launch emits candidate lists");
   const int row = SLICED ? (int)blockIdx.x / p.n_slices : (int)blockIdx.x;
@@ -2166,7 +2169,22 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         // the buffer and compacts it several times before any threshold exists.
         // (256-thread and shard or slice launches: the 512-thread row kernel has no register
         // left for it at two workgroups per CU)
-        if constexpr (EMIT || NT < TOPK_NT) {
+        // SEED takes four offers a lane, so each wave's bound is near its own top_k-th largest
+        // logit, and the largest of the waves' bounds (each at most the row's top_k-th
+        // largest z) lets about top_k elements of the batch through instead of every
+        // wave's share.  The condition is uniform over the workgroup (tau is, once set).
+        if constexpr (SEED) {
+          if (p.top_k >= 1 && p.top_k <= 4 * 64 && !(tau > NEG_INF)) {
+            float tw = NEG_INF;
+            seed_tau<4, NT>(x, t0, h, p, tw);
+            if (lane == 0) m->rf[wid] = tw;
+            __syncthreads();
+            float tb = NEG_INF;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) tb = fmaxf(tb, m->rf[i]);
+            tau = uni(tb);
+          }
+        } else if constexpr (EMIT || NT < TOPK_NT) {
           if (p.top_k >= 1 && p.top_k <= 64 && !(tau > NEG_INF)) seed_tau<1, NT>(x, t0, h, p, tau);
         }
         // (skipped when no lane holds a finite value: the maximum is then unchanged; the
@@ -3239,6 +3257,11 @@ __global__ __launch_bounds__(256) void full_finish_kernel(dsv41_sampler_full_fin
 }
 
 // ====================================================================== host
+// 256-thread row launches of top_k <= 256 without min-p take topk_kernel<..., SEED>
+inline bool topk_seeded(const Params& q, int nt) {
+  return nt == 256 && q.top_k >= 1 && q.top_k <= 256 && !(q.min_p > 0.0f);
+}
+
 template <class K>
 int launch(K kernel, int nt, size_t lds, int rows, const Params& prm, hipStream_t stream) {
   DSV41_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -3486,7 +3509,13 @@ Params make_params(const dsv41_sampler_desc* d, const Plan& pl, void* workspace)
   p.hlen = d->hist_len;
   p.top_k = pl.internal_k ? INTERNAL_K : d->top_k;
   p.topk_internal = pl.internal_k ? 1 : 0;
-  p.mid_trigger = pl.internal_k ? INT_MAX : 2 * d->top_k + 128;
+  // Seeded 256-thread batches of a small top_k compact sooner: their threshold rises only
+  // at a compaction, and below top_k 128 a fresher threshold saves more passers than the
+  // extra compactions cost (E's shape: top-k 50 563 -> 534 us with top_k + 64 instead of
+  // 2 top_k + 128; top-k 200 and 256 measured slower with the lower trigger).
+  p.mid_trigger = pl.internal_k ? INT_MAX
+                  : topk_seeded(p, pl.topk_nt) && d->top_k < 128 ? d->top_k + std::min(std::max(d->top_k, 32), 64)
+                                                                 : 2 * d->top_k + 128;
   p.greedy = d->greedy ? 1 : 0;
   p.has_pen = pl.has_pen ? 1 : 0;
   p.pen_lowers = pl.has_pen && d->repetition_penalty >= 1.0f && d->presence_penalty >= 0.0f &&
@@ -3596,7 +3625,13 @@ static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params
 // the batch gathers no history slots (no penalties, or lowering penalties).
 template <typename TIn, bool VEC, int NT>
 static int launch_topk_rows(size_t lds, int rows, const Params& q, hipStream_t s) {
-  if (q.has_pen && !q.pen_lowers) return launch(topk_kernel<TIn, VEC, false, NT>, NT, lds, rows, q, s);
+  const bool gather = q.has_pen && !q.pen_lowers;
+  if constexpr (NT == 256) {
+    if (topk_seeded(q, NT))
+      return gather ? launch(topk_kernel<TIn, VEC, false, NT, false, true, true>, NT, lds, rows, q, s)
+                    : launch(topk_kernel<TIn, VEC, false, NT, false, false, true>, NT, lds, rows, q, s);
+  }
+  if (gather) return launch(topk_kernel<TIn, VEC, false, NT>, NT, lds, rows, q, s);
   return launch(topk_kernel<TIn, VEC, false, NT, false, false>, NT, lds, rows, q, s);
 }
 
