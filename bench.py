@@ -232,7 +232,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: every GPU box here has one "
-              "GPU, and rows and tokens shard with no exchange (DESIGN.md, 'More than one GPU')",
+              "GPU, and the sampler's rows and the log-prob's tokens shard across GPUs with no exchange",
               file=sys.stderr)
         sys.exit(2)
     import torch
