@@ -2189,7 +2189,10 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
         }
         // (skipped when no lane holds a finite value: the maximum is then unchanged; the
         // test costs the unaligned-row instantiations their fourth wave per SIMD)
-        if (!VEC || __ballot(zmx > NEG_INF)) wm = uni(fmaxf(wm, wave_max_dpp(zmx)));
+        // (SEED launches have no min-p, the one use of the running maximum: they keep none)
+        if constexpr (!SEED) {
+          if (!VEC || __ballot(zmx > NEG_INF)) wm = uni(fmaxf(wm, wave_max_dpp(zmx)));
+        }
         const float bnd = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
         if (!(tau == c_tau && bnd == c_bnd)) {
           c_tau = tau;
@@ -2267,7 +2270,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
               }
             }
           }
-          wm = uni(fmaxf(wm, wave_max_dpp(pz)));
+          if constexpr (!SEED) wm = uni(fmaxf(wm, wave_max_dpp(pz)));
         }
         // the batch's gathered history slot (none when the batch gathered none: zg = -inf)
         uint64_t kg = 0;
@@ -2327,7 +2330,7 @@ __global__ __launch_bounds__(NTK) void topk_kernel(Params p) {
             z2 = pen_z(load_one<TIn>(rs, (int)t2), count_of(h, s), p);
             if (!isfinite(z2)) bad = 1;
           }
-          wm = uni(fmaxf(wm, wave_max_dpp(z2)));
+          if constexpr (!SEED) wm = uni(fmaxf(wm, wave_max_dpp(z2)));
           const float bnd2 = minp_bound_f(fmaxf(wm, mblk), p.lmin_f);
           const uint64_t k2 = ckey(z2, t2), tk3 = tau_key;
           round([&](int, uint64_t& key) {
