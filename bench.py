@@ -60,8 +60,9 @@ def parse():
     # steady state (20 steps after 5 read several percent slow on a fresh box).
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="E", choices=["A", "B", "E", "E_full", "none"],
-                    help="headline sampler config; 'none' runs only the log-prob leg (for profiling)")
+    ap.add_argument("--workload", default="E", choices=["A", "B", "E", "E_full", "E_topp", "E_topk50", "none"],
+                    help="headline sampler config; E_full / E_topp / E_topk50: E's logits in another "
+                         "mode (no penalties); 'none' runs only the log-prob leg (for profiling)")
     ap.add_argument("--logprob", default="D", choices=["C", "D", "none"])
     ap.add_argument("--logprob-steps", type=int, default=10)
     ap.add_argument("--no-backward", action="store_true", help="skip the log-prob backward timing")
@@ -93,18 +94,28 @@ def copy_calibration(nbytes, steps, torch):
     print(json.dumps({"copy_bytes": nbytes, "ms": ms, "GBps": 2 * nbytes / ms / 1e6}), flush=True)
 
 
-def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0, full=False):
-    """One sampler configuration.  ``full``: the training-default mode on the configuration's
-    logits (rollout_manager/training.py:74-81): the temperature alone, no penalties and no
-    truncation, so a full-vocabulary inverse-CDF draw."""
+# Other modes on a configuration's logits: its temperature, no penalties, and these knobs.
+#   full: the training default (rollout_manager/training.py:74-81), no truncation, so a
+#         full-vocabulary inverse-CDF draw;
+#   topp, topk50: serving mixes the reference forwards to vLLM (rollout_manager/backends/
+#         vllm_actor.py:178-185): top-p 0.9 alone, top-k 50 alone.
+SAMPLER_MODES = {
+    "full": ({}, "training-default full-vocabulary inverse CDF"),
+    "topp": ({"top_p": 0.9}, "top-p 0.9 alone, no penalties"),
+    "topk50": ({"top_k": 50}, "top-k 50 alone, no penalties"),
+}
+
+
+def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0, mode=None):
+    """One sampler configuration, or the configuration's logits in one of SAMPLER_MODES."""
     from dsv41_rocm import _lib, workloads
 
     dev = torch.device("cuda:0")
     print(f"[bench] generating sampler config {name} on the GPU", file=sys.stderr, flush=True)
     inp = workloads.sampler_inputs(name, device=dev)
     logits, history, uniforms, knobs = inp["logits"], inp["history"], inp["uniforms"], inp["knobs"]
-    if full:
-        knobs = {"temperature": knobs.get("temperature", 1.0)}
+    if mode:
+        knobs = {"temperature": knobs.get("temperature", 1.0), **SAMPLER_MODES[mode][0]}
         history = history[:, :0]
         inp = dict(inp, history=history, knobs=knobs)
     rows, vocab = logits.shape
@@ -167,11 +178,11 @@ def bench_sampler(name, steps, warmup, cpu_baseline, torch, cpu_seconds=10.0, fu
         "data": "synthetic",
         "config": {"workload": f"{name}: sampler {rows}x{vocab} "
                                f"{'fp32' if esize == 4 else 'bf16'}, history {history.shape[1]}"
-                               + (", training-default full-vocabulary inverse CDF" if full else ""),
+                               + (f", {SAMPLER_MODES[mode][1]}" if mode else ""),
                    "rows": rows, "vocab": vocab, "hist_len": history.shape[1], **knobs},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": MEASURED_TRAFFIC.get(f"sampler_{name}" + ("_full" if full else "")),
+                     "traffic": MEASURED_TRAFFIC.get(f"sampler_{name}" + (f"_{mode}" if mode else "")),
                      "bytes_per_row": per_row},
         "steady_state": {"steps": steady_steps, "ms_per_step": steady_ms,
                          "rows_per_s": rows / (steady_ms * 1e-3),
@@ -245,7 +256,7 @@ def main():
         line = {}
     else:
         line = bench_sampler(args.workload.split("_")[0], args.steps, args.warmup, cpu, torch,
-                             full=args.workload.endswith("_full"))
+                             mode=args.workload.split("_", 1)[1] if "_" in args.workload else None)
         print(json.dumps({k: line[k] for k in ("value", "unit", "ms_per_step")}), file=sys.stderr, flush=True)
     if args.logprob != "none":
         line["logprob"] = bench_logprob(args.logprob, args.logprob_steps, 3, cpu, torch,
@@ -256,7 +267,7 @@ def main():
             if name != args.workload:
                 extra[f"sampler_{name}"] = bench_sampler(name, 200, 20, cpu, torch, cpu_seconds=4.0)
                 print(json.dumps({name: extra[f"sampler_{name}"]["ms_per_step"]}), file=sys.stderr, flush=True)
-        extra["sampler_E_full"] = bench_sampler("E", 100, 20, cpu, torch, cpu_seconds=4.0, full=True)
+        extra["sampler_E_full"] = bench_sampler("E", 100, 20, cpu, torch, cpu_seconds=4.0, mode="full")
         print(json.dumps({"E_full": extra["sampler_E_full"]["ms_per_step"]}), file=sys.stderr, flush=True)
         if args.logprob != "C":
             extra["logprob_C"] = bench_logprob("C", 20, 3, cpu, torch, backward=False)

@@ -51,6 +51,7 @@ constexpr int MODE_TOPP = 3;
 constexpr int FULL_NT = 1024;
 constexpr int TOPK_NT = 512;
 constexpr int GEN_NT = 1024;
+constexpr int FALLBACK_GRID = 512;             // generic_kernel workgroups of a fallback launch
 constexpr int MAX_NW = 16;
 constexpr int PF = 4;                          // tiles per pipelined batch
 constexpr int TOPK_G = 4;                      // elements per thread per TOPK tile
@@ -154,7 +155,7 @@ struct Params {
   dsv41_full_pick* sh_out_picks;
   const uint64_t* sh_masses;  // [n_shards, nrows] gathered exact masses (DRAW_SHARD_CDF)
   uint64_t* sh_out_masses;    // [nrows] (DRAW_SHARD_MASS)
-  int n_shards, shard_index, nrows;
+  int n_shards, shard_index, nrows;  // nrows: the batch's rows (also generic_kernel's fallback launch)
   // sliced small batch (topk_kernel<..., EMIT, NTK, SLICED>): workgroup b takes slice
   // b % n_slices (slice_w ids from slice * slice_w) of row b / n_slices
   int n_slices, slice_w;
@@ -2437,136 +2438,151 @@ __global__ __launch_bounds__(GEN_NT) void generic_kernel(Params p) {
   const Hist h = hist_tables(smem, L);
   uint64_t* hist = reinterpret_cast<uint64_t*>(smem + L.hist256);
 
-  const int row = blockIdx.x, tid = threadIdx.x;
-  if (p.only_flagged && !(p.out_status[row] & ST_FALLBACK)) return;
-  HistIds<HR> hi;
-  load_history<NT, HR>(p, row, hi);
-  const TIn* src = row_ptr<TIn>(p, row);
-  const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
-  float* zr = p.zbuf + (int64_t)row * p.V;
-  constexpr int TILE = NT * G;
-  int bad = 0;
-  int U = 0;
-  stream_row<TIn, G, NT, VEC, false>(
-      p, rs, h,
-      [&]() {
-        if (tid == 0) m->status = 0;
-        __syncthreads();
-        if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
-        landed(hi);  // the ids are read under conditions; end their loads on every path
-        return U;
-      },
-      [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
-#pragma unroll
-        for (int k = 0; k < PF; ++k) {
-          const int t = t0 + k;
-          if (t < nt) {
-            const int base = t * TILE + tid * G;
-            float x[G], z[G];
-            unpack(R[k], x);
-            make_z<G, true>(x, base, p, h.bitmap, z, bad);
-#pragma unroll
-            for (int j = 0; j < G; ++j)
-              if (base + j < p.V) zr[base + j] = z[j];
-          }
-        }
-        // the tiles wrote -inf at history tokens: order those stores before the exact ones
-        __threadfence_block();
-        __syncthreads();
-        for (int i = tid; i < n; i += NT) {
-          const int s = s0 + i;
-          const float x = i == tid ? gx : load_one<TIn>(rs, (int)h.tok[s]);
-          const float z = pen_z(x, count_of(h, s), p);
-          if (!isfinite(z)) bad = 1;
-          zr[h.tok[s]] = z;
-        }
-      });
-  if (bad) atomicOr(&m->status, ST_NONFINITE);
-  __threadfence_block();
-  __syncthreads();
-
-  const int V = p.V;
-  float bm = NEG_INF;
-  int bi = 0x7FFFFFFF;
-  for (int i = tid; i < V; i += NT) {
-    const float z = zr[i];
-    if (z > bm) {
-      bm = z;
-      bi = i;
-    }
+  const int tid = threadIdx.x;
+  // One row per workgroup.  A fallback launch (only_flagged, after TOPK or TOPP) walks the
+  // batch with a grid of at most FALLBACK_GRID workgroups and redoes only the flagged rows,
+  // which are few: a row per workgroup would dispatch the whole batch to find them.
+  const int nrows = p.only_flagged ? p.nrows : (int)gridDim.x;
+  if (p.only_flagged) {
+    // this workgroup's rows' statuses in one parallel read; most launches find none flagged
+    const int mine = ((nrows - (int)blockIdx.x) + (int)gridDim.x - 1) / (int)gridDim.x;
+    bool flagged = mine > NT;  // (more rows than threads: the loop reads the rest itself)
+    for (int j = tid; j < mine && j < NT; j += NT)
+      flagged |= (p.out_status[blockIdx.x + j * gridDim.x] & ST_FALLBACK) != 0;
+    if (block_sum_i<NT>(flagged ? 1 : 0, m) == 0) return;  // (no static LDS: the launch sets the dynamic maximum)
   }
-  const float zmax = block_max<NT>(bm, m);
-  int am = block_min_i<NT>(bm == zmax ? bi : 0x7FFFFFFF, m);
-  if (am < 0 || am >= V) am = 0;  // no finite maximum: the row is flagged non-finite
-  const float u = row_uniform(p, row, m);
-
-  int el = 0;
-  for (int i = tid; i < V; i += NT) el += minp_ok(zr[i], zmax, p) ? 1 : 0;
-  el = block_sum_i<NT>(el, m);
-  const int K = (p.top_k > 0 && p.top_k < el) ? p.top_k : el;
-  bool found = false;
-  uint64_t B1 = 0;
-  if (K < el) {
-    B1 = radix_select<NT, true, 64>(
-        [&](auto&& f) {
-          for (int i = tid; i < V; i += NT) {
-            const float z = zr[i];
-            if (minp_ok(z, zmax, p)) f(ckey(z, (uint32_t)i), 1ull);
-          }
+  for (int row = blockIdx.x; row < nrows; row += gridDim.x) {
+    if (p.only_flagged && !(p.out_status[row] & ST_FALLBACK)) continue;  // uniform: one row
+    HistIds<HR> hi;
+    load_history<NT, HR>(p, row, hi);
+    const TIn* src = row_ptr<TIn>(p, row);
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
+    float* zr = p.zbuf + (int64_t)row * p.V;
+    constexpr int TILE = NT * G;
+    int bad = 0;
+    int U = 0;
+    stream_row<TIn, G, NT, VEC, false>(
+        p, rs, h,
+        [&]() {
+          if (tid == 0) m->status = 0;
+          __syncthreads();
+          if (p.has_pen) U = build_history<NT, HR>(p, row, hi, h, m);
+          landed(hi);  // the ids are read under conditions; end their loads on every path
+          return U;
         },
-        (uint64_t)K, hist, m, &found);
-  }
-  uint64_t B = B1;
-  if (p.top_p < 1.0f) {
-    uint64_t s1 = 0;
+        [&](int t0, int nt, Raw<TIn, G>(&R)[PF], int s0, int n, float gx) {
+  #pragma unroll
+          for (int k = 0; k < PF; ++k) {
+            const int t = t0 + k;
+            if (t < nt) {
+              const int base = t * TILE + tid * G;
+              float x[G], z[G];
+              unpack(R[k], x);
+              make_z<G, true>(x, base, p, h.bitmap, z, bad);
+  #pragma unroll
+              for (int j = 0; j < G; ++j)
+                if (base + j < p.V) zr[base + j] = z[j];
+            }
+          }
+          // the tiles wrote -inf at history tokens: order those stores before the exact ones
+          __threadfence_block();
+          __syncthreads();
+          for (int i = tid; i < n; i += NT) {
+            const int s = s0 + i;
+            const float x = i == tid ? gx : load_one<TIn>(rs, (int)h.tok[s]);
+            const float z = pen_z(x, count_of(h, s), p);
+            if (!isfinite(z)) bad = 1;
+            zr[h.tok[s]] = z;
+          }
+        });
+    if (bad) atomicOr(&m->status, ST_NONFINITE);
+    __threadfence_block();
+    __syncthreads();
+
+    const int V = p.V;
+    float bm = NEG_INF;
+    int bi = 0x7FFFFFFF;
     for (int i = tid; i < V; i += NT) {
       const float z = zr[i];
-      if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B1) s1 += mass_of(z, zmax);
+      if (z > bm) {
+        bm = z;
+        bi = i;
+      }
     }
-    s1 = block_sum_u64<NT>(s1, m);
-    const uint64_t thr = top_p_threshold(p.top_p, s1);
-    B = radix_select<NT, true, 64>(
-        [&](auto&& f) {
-          for (int i = tid; i < V; i += NT) {
-            const float z = zr[i];
-            const uint64_t k = ckey(z, (uint32_t)i);
-            if (minp_ok(z, zmax, p) && k >= B1) f(k, mass_of(z, zmax));
-          }
-        },
-        thr, hist, m, &found);
-    if (!found) B = B1;
-  }
-  int nk = 0;
-  uint64_t sk = 0;
-  double es = 0.0;
-  for (int i = tid; i < V; i += NT) {
-    const float z = zr[i];
-    if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B) {
-      ++nk;
-      sk += mass_of(z, zmax);
-      es += exp_det((double)z - (double)zmax);
+    const float zmax = block_max<NT>(bm, m);
+    int am = block_min_i<NT>(bm == zmax ? bi : 0x7FFFFFFF, m);
+    if (am < 0 || am >= V) am = 0;  // no finite maximum: the row is flagged non-finite
+    const float u = row_uniform(p, row, m);
+
+    int el = 0;
+    for (int i = tid; i < V; i += NT) el += minp_ok(zr[i], zmax, p) ? 1 : 0;
+    el = block_sum_i<NT>(el, m);
+    const int K = (p.top_k > 0 && p.top_k < el) ? p.top_k : el;
+    bool found = false;
+    uint64_t B1 = 0;
+    if (K < el) {
+      B1 = radix_select<NT, true, 64>(
+          [&](auto&& f) {
+            for (int i = tid; i < V; i += NT) {
+              const float z = zr[i];
+              if (minp_ok(z, zmax, p)) f(ckey(z, (uint32_t)i), 1ull);
+            }
+          },
+          (uint64_t)K, hist, m, &found);
     }
-  }
-  nk = block_sum_i<NT>(nk, m);
-  sk = block_sum_u64<NT>(sk, m);
-  const double esum = block_sum_d<NT>(es, m);
-  int64_t tok = am;
-  if (!p.greedy) {
-    const uint64_t t = draw_target(u, sk);
-    const uint64_t idx = radix_select<NT, false, 24>(
-        [&](auto&& f) {
-          for (int i = tid; i < V; i += NT) {
-            const float z = zr[i];
-            if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B) f((uint64_t)i, mass_of(z, zmax));
-          }
-        },
-        t + 1, hist, m, &found);
-    if (found) tok = (int64_t)idx;
-  }
-  if (tid == 0) {
-    const float ztok = zr[tok];
-    const float lp = (float)(((double)ztok - (double)zmax) - log(esum));
-    write_result(p, row, m, tok, lp, nk);
+    uint64_t B = B1;
+    if (p.top_p < 1.0f) {
+      uint64_t s1 = 0;
+      for (int i = tid; i < V; i += NT) {
+        const float z = zr[i];
+        if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B1) s1 += mass_of(z, zmax);
+      }
+      s1 = block_sum_u64<NT>(s1, m);
+      const uint64_t thr = top_p_threshold(p.top_p, s1);
+      B = radix_select<NT, true, 64>(
+          [&](auto&& f) {
+            for (int i = tid; i < V; i += NT) {
+              const float z = zr[i];
+              const uint64_t k = ckey(z, (uint32_t)i);
+              if (minp_ok(z, zmax, p) && k >= B1) f(k, mass_of(z, zmax));
+            }
+          },
+          thr, hist, m, &found);
+      if (!found) B = B1;
+    }
+    int nk = 0;
+    uint64_t sk = 0;
+    double es = 0.0;
+    for (int i = tid; i < V; i += NT) {
+      const float z = zr[i];
+      if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B) {
+        ++nk;
+        sk += mass_of(z, zmax);
+        es += exp_det((double)z - (double)zmax);
+      }
+    }
+    nk = block_sum_i<NT>(nk, m);
+    sk = block_sum_u64<NT>(sk, m);
+    const double esum = block_sum_d<NT>(es, m);
+    int64_t tok = am;
+    if (!p.greedy) {
+      const uint64_t t = draw_target(u, sk);
+      const uint64_t idx = radix_select<NT, false, 24>(
+          [&](auto&& f) {
+            for (int i = tid; i < V; i += NT) {
+              const float z = zr[i];
+              if (minp_ok(z, zmax, p) && ckey(z, (uint32_t)i) >= B) f((uint64_t)i, mass_of(z, zmax));
+            }
+          },
+          t + 1, hist, m, &found);
+      if (found) tok = (int64_t)idx;
+    }
+    if (tid == 0) {
+      const float ztok = zr[tok];
+      const float lp = (float)(((double)ztok - (double)zmax) - log(esum));
+      write_result(p, row, m, tok, lp, nk);
+    }
+    __syncthreads();  // this row's last reads of LDS before the next row's tables
   }
 }
 
@@ -3607,20 +3623,22 @@ static int run_sliced(const dsv41_sampler_desc* d, const Plan& pl, const Params&
 }
 
 // Rows flagged ST_FALLBACK by topk_kernel (more min-p survivors than the internal bound)
-// or topp_kernel (a boundary bin above TOPP_CAP) again, with generic_kernel; every other
-// row returns at once.
+// or topp_kernel (a boundary bin above TOPP_CAP) again, with generic_kernel: at most
+// FALLBACK_GRID workgroups read the statuses and redo the flagged rows.
 static int run_flagged(const dsv41_sampler_desc* d, const Plan& pl, const Params& p, hipStream_t s) {
   Params g = p;
   g.top_k = d->top_k;
   g.topk_internal = 0;
   g.only_flagged = 1;
+  g.nrows = d->rows;
   g.defer = 0;
   g.cap = 0;
   const size_t lds = make_layout<MODE_GENERIC, 4>(d->vocab, pl.words, pl.ucap, 0).total;
-  if (pl.esize == 2) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, lds, d->rows, g, s)
-                                   : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, lds, d->rows, g, s);
-  return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, lds, d->rows, g, s)
-                : launch(generic_kernel<float, 4, false>, GEN_NT, lds, d->rows, g, s);
+  const int grid = std::min(d->rows, FALLBACK_GRID);
+  if (pl.esize == 2) return pl.vec ? launch(generic_kernel<uint16_t, 4, true>, GEN_NT, lds, grid, g, s)
+                                   : launch(generic_kernel<uint16_t, 4, false>, GEN_NT, lds, grid, g, s);
+  return pl.vec ? launch(generic_kernel<float, 4, true>, GEN_NT, lds, grid, g, s)
+                : launch(generic_kernel<float, 4, false>, GEN_NT, lds, grid, g, s);
 }
 
 // A small FULL batch: the slices' statistics, then one finishing workgroup per row.
