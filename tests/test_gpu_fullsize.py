@@ -6,6 +6,8 @@ plans of the benchmark runs themselves are checked:
   8 x 4 XCD super-tiles, forward with the Token-TIS ratio and the logit gradient;
 * C (8192 tokens x 2048 -> 151936): 32 token blocks x 8 splits;
 * E (4096 x 151936 fp32): 256-thread top-k workgroups with the deferred final selection;
+  E's logits with top-p 0.9 alone (512-thread top-p workgroups) and top-k 50 alone (the
+  seeded top-k instantiation);
 * a 2048 x 136 -> 8192 head, small enough to check every logit gradient, on the same 8 x 4
   super-tile mapping (8 token blocks x 32 splits).
 
@@ -161,4 +163,34 @@ def test_config_e_full_size_sampler():
     np.testing.assert_array_equal(gids, oids)
     d_lp = np.max(np.abs(glp - olp))
     print(f"config E: 4096 rows, ids and kept sets identical, max|lp - oracle| {d_lp:.3e}", flush=True)
+    assert d_lp <= TOL
+
+
+@pytest.mark.parametrize("mode", ["top_p", "top_k"])
+def test_config_e_shape_serving_mixes(mode):
+    """E's 4096 rows in two serving mixes, on the launch plans of the opt-in bench workloads:
+    top-p 0.9 alone (topp_kernel with 512 threads, two workgroups per CU) and top-k 50 alone
+    (the seeded 256-thread topk_kernel and the deferred selection).  The oracle runs over row
+    blocks in threads (ctypes releases the GIL): top-p alone sorts every row."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    inp = workloads.sampler_inputs("E", device=DEV)
+    logits, uniforms = inp["logits"], inp["uniforms"]
+    knobs = dict(temperature=0.6, **(dict(top_p=0.9) if mode == "top_p" else dict(top_k=50)))
+    print(f"case: config E's logits {tuple(logits.shape)} knobs={knobs}", flush=True)
+    res = sample(logits, uniforms=uniforms, check=False, **knobs)
+    torch.cuda.synchronize()
+    gids, glp, gkept, gst = (r.cpu().numpy() for r in (res.ids, res.logprobs, res.kept, res.status))
+    x, u = logits.cpu().numpy(), uniforms.cpu().numpy()
+    cuts = np.linspace(0, x.shape[0], 17).astype(int)
+    with ThreadPoolExecutor(16) as ex:
+        parts = list(ex.map(lambda ab: oracle.sample(x[ab[0]:ab[1]], uniforms=u[ab[0]:ab[1]], **knobs),
+                            zip(cuts[:-1], cuts[1:])))
+    oids, olp, okept, ost = (np.concatenate([p[i] for p in parts]) for i in range(4))
+    np.testing.assert_array_equal(gst, ost)
+    assert (ost == 0).all()
+    np.testing.assert_array_equal(gkept, okept)
+    np.testing.assert_array_equal(gids, oids)
+    d_lp = np.max(np.abs(glp - olp))
+    print(f"config E's logits, {mode}: ids and kept sets identical, max|lp - oracle| {d_lp:.3e}", flush=True)
     assert d_lp <= TOL
