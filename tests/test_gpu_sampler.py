@@ -485,6 +485,24 @@ def test_top_p_alone_two_workgroups_per_cu(rows, V, dtype, hist_len):
     assert (gpu[2][3::8][gpu[3][3::8] == 0] > 4096).all()
 
 
+@pytest.mark.parametrize("top_p", [0.01, 0.999, float(np.nextafter(np.float32(1.0), np.float32(0.0)))])
+def test_top_p_alone_depth_bound_extremes(top_p):
+    """Tokens below ln((1 - p) / V) cannot hold the boundary, so only those above it are
+    binned.  The extremes of that depth: p = 0.01 (the boundary at the maximum's own token
+    in most rows) and the largest float below 1 (the depth at its floor of -31, every token
+    with mass binned), on 520 rows of 20011 ids (512-thread workgroups): peaked, flat, tied
+    and constant rows."""
+    g = torch.Generator().manual_seed(7)
+    rows, V = 520, 20011
+    logits = 3.0 * torch.randn(rows, V, generator=g)
+    logits[1::4] = 0.01 * torch.randn(len(range(1, rows, 4)), V, generator=g)
+    logits[2::4] = torch.randint(-4, 5, (len(range(2, rows, 4)), V), generator=g).float()
+    logits[3::8] = 0.25
+    u = torch.rand(rows, generator=g)
+    gpu, ora = run_both(logits, u, temperature=0.7, top_p=top_p)
+    assert_exact(gpu, ora)
+
+
 def test_top_p_alone_config_e_vocabulary():
     inp = workloads.sampler_inputs("E", rows=64)
     gpu, ora = run_both(inp["logits"], inp["uniforms"], inp["history"], temperature=0.6,
