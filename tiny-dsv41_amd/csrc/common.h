@@ -136,6 +136,25 @@ __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
   v += dpp_scan_u64<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
   return v;
 }
+// fp64 sum over the 64 lanes (all lanes active), the same value in every lane: the DPP
+// inclusive scan above on the double's bits (lanes whose source lies outside read +0.0),
+// then lane 63's total.  Its order is fixed, so the sum is deterministic.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_scan_d(double v) {
+  return __builtin_bit_cast(double, dpp_scan_u64<CTRL, ROWS>(__builtin_bit_cast(uint64_t, v)));
+}
+__device__ __forceinline__ double wave_total_d(double v) {
+  v += dpp_scan_d<0x111>(v);        // row_shr:1
+  v += dpp_scan_d<0x112>(v);        // row_shr:2
+  v += dpp_scan_d<0x114>(v);        // row_shr:4
+  v += dpp_scan_d<0x118>(v);        // row_shr:8
+  v += dpp_scan_d<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_scan_d<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ int wave_incl_scan_i(int v, int lane) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {

@@ -1845,7 +1845,9 @@ __device__ __forceinline__ uint64_t wave_rank_desc(uint64_t v, uint64_t* buf, in
 // same decisions as the workgroup path (min-p, top-k, top-p over exact integer masses,
 // inverse-CDF draw in vocabulary order), with every step in registers.  cand (LDS, this
 // wave's to overwrite) holds the keys; with R = 1 the two sorts go by rank through it.
-template <int R>
+// DPP: the kept set's fp64 exp sum by the DPP scan (select_kernel and merge_kernel; the
+// in-place copy in topk_kernel keeps the shuffle sum, which leaves that kernel's code as it is)
+template <int R, bool DPP = false>
 __device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, uint64_t* cand, int n, float u) {
   const int lane = threadIdx.x & 63;
   uint64_t k[R];
@@ -1887,7 +1889,7 @@ __device__ __forceinline__ void wave_final(const Params& p, int row, Misc* m, ui
 #pragma unroll
   for (int r = 0; r < R; ++r)
     if (r * 64 + lane < n_keep) es += exp_det((double)ckey_z(k[r]) - (double)zmax);
-  const double esum = wave_sum_d(es);
+  const double esum = DPP ? wave_total_d(es) : wave_sum_d(es);
   int64_t tok = (int64_t)ckey_idx(k0);
   float ztok = zmax;
   if (!p.greedy) {
@@ -3039,19 +3041,15 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int ro
   }
   constexpr int RK = DEFER_KEYS / 64;
   uint64_t k[RK];
-  uint64_t kmax = 0;
+  float zl = NEG_INF;
 #pragma unroll
   for (int r = 0; r < RK; ++r) {
     k[r] = r * 64 + lane < n ? (r == 0 ? first : keys[r * 64 + lane]) : 0;  // 0 is below every key
-    kmax = k[r] > kmax ? k[r] : kmax;
+    if (r * 64 + lane < n) zl = fmaxf(zl, ckey_z(k[r]));
   }
-  // the largest key: its z is the row maximum the selection measures min-p against
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t t = __shfl_xor(kmax, o);
-    kmax = t > kmax ? t : kmax;
-  }
-  const float zmax = ckey_z(kmax);
+  // the row maximum the selection measures min-p against: the largest key's z, which is the
+  // largest of the keys' z (the key order puts z first)
+  const float zmax = wave_max_dpp(zl);
   uint64_t* buf = kept_keys[wid];
   int el = 0;
 #pragma unroll
@@ -3064,9 +3062,9 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_kernel(Params p, int ro
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (el <= 64) wave_final<1>(p, row, m, buf, el, u);
-  else if (el <= 128) wave_final<2>(p, row, m, buf, el, u);
-  else wave_final<4>(p, row, m, buf, el, u);
+  if (el <= 64) wave_final<1, true>(p, row, m, buf, el, u);
+  else if (el <= 128) wave_final<2, true>(p, row, m, buf, el, u);
+  else wave_final<4, true>(p, row, m, buf, el, u);
 }
 
 // One workgroup per row of a vocabulary-sharded batch: the final selection over the
@@ -3184,7 +3182,7 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const float u = row_uniform(p, row, m);
-        wave_final<1>(p, row, m, cand, n, u);
+        wave_final<1, true>(p, row, m, cand, n, u);
       }
       return;
     }
@@ -3204,9 +3202,9 @@ __global__ __launch_bounds__(TOPK_NT) void merge_kernel(Params p, MergeIn in) {
   if (n >= 1 && n <= 4 * 64) {
     if (wid == 0) {
       const float u = row_uniform(p, row, m);
-      if (n <= 64) wave_final<1>(p, row, m, cand, n, u);
-      else if (n <= 128) wave_final<2>(p, row, m, cand, n, u);
-      else wave_final<4>(p, row, m, cand, n, u);
+      if (n <= 64) wave_final<1, true>(p, row, m, cand, n, u);
+      else if (n <= 128) wave_final<2, true>(p, row, m, cand, n, u);
+      else wave_final<4, true>(p, row, m, cand, n, u);
     }
     return;
   }
