@@ -2653,11 +2653,14 @@ __global__ __launch_bounds__(NT, 4) void topp_kernel(Params p) {
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(src, (uint32_t)p.V * (uint32_t)sizeof(TIn));
   const int V = p.V;
 
-  // ---- pass 1: maximum and its first index
+  // ---- pass 1: maximum and its first index.  Its loads keep the default cache policy
+  // (not the streams' non-temporal one): the second pass reads the same lines tens of
+  // microseconds later, and some are still in the Infinity Cache (E's shape, top-p 0.9:
+  // 1010 -> 991 us)
   int bad = 0, U = 0;
   float bm = NEG_INF;
   int bi = 0x7FFFFFFF;
-  stream_row<TIn, G, NT, VEC, false>(
+  stream_row<TIn, G, NT, VEC, false, 0>(
       p, rs, h,
       [&]() {
         if (tid == 0) {
